@@ -1,0 +1,292 @@
+#!/usr/bin/env python3
+"""Benchmark of the qkern hot path on one MI355X.
+
+Headline (`value`): int4 group-64 GEMV throughput at the Qwen3-8B decode
+projection shapes (M = 1; N x K = 4096x4096, 12288x4096, 4096x12288 and the
+151936x4096 lm_head), the first half of BASELINE.json's metric. One step =
+one qk$qmatvec launch per shape, weights already resident in HBM. Three
+copies of the weight set (1.25 GB) are rotated so that no launch reads
+weights another launch left in the 256 MB Infinity Cache.
+
+Also reported (`secondary`): bf16 GEMM + bias + SiLU TFLOP/s at the C3
+shapes (the metric's second half), int4 M = 16 / 512, int8 affine GEMV,
+RMSNorm and softmax [4096, 4096] HBM GB/s; each against its roofline.
+
+Timing: HIP events recorded on the stream the kernels are launched on
+(torch's current stream, which qkern launches on), W untimed warm-up steps,
+then K timed steps bracketed by torch.cuda.synchronize().
+
+CPU baseline: the oracle's C port of the reference's _matvec_int4
+(oracle/qk_oracle.c, float32, OpenMP over output rows) on the host cores,
+on a bounded sample of the same workload.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "metal-pjrt-plugin_amd"))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0  # dense MFMA
+QWEN3_8B = [(4096, 4096), (12288, 4096), (4096, 12288), (151936, 4096)]
+GROUP = 64
+
+
+def int4_bytes(m, n, k):
+    """Algorithmic bytes of one int4 g64 qmatvec: codes (K/2 B per row),
+    bf16 scale + bias per group, x and y in bf16, each read/written once."""
+    return n * k // 2 + n * (k // GROUP) * 4 + m * k * 2 + m * n * 2
+
+
+def int8_bytes(m, n, k):
+    return n * k + n * (k // GROUP) * 4 + m * k * 2 + m * n * 2
+
+
+def make_int4(torch, dev, n, k, gen):
+    words = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k // 8), dtype=torch.int32,
+                          device=dev, generator=gen)
+    s = (torch.rand(n, k // GROUP, device=dev, generator=gen) * 0.019 +
+         0.001).to(torch.bfloat16)
+    b = (0.05 * torch.randn(n, k // GROUP, device=dev, generator=gen)).to(
+        torch.bfloat16)
+    return words, s, b
+
+
+def timed_launches(torch, fn, iters):
+    """Average device time (ms) per call of fn over `iters` calls, from HIP
+    events on the current stream around each call."""
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    torch.cuda.synchronize()
+    for i in range(iters):
+        starts[i].record()
+        fn(i)
+        ends[i].record()
+    torch.cuda.synchronize()
+    return sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / iters
+
+
+def secondary(torch, qkern, dev, gen):
+    out = []
+    # bf16 GEMM + bias + SiLU (C3), NN row-major: D = silu(A @ B + bias)
+    for (m, n, k) in [(4096, 4096, 4096), (2048, 12288, 4096),
+                      (2048, 4096, 12288)]:
+        a = (torch.randn(m, k, device=dev, generator=gen) / k ** 0.5).to(
+            torch.bfloat16)
+        b = (torch.randn(k, n, device=dev, generator=gen) / k ** 0.5).to(
+            torch.bfloat16)
+        bias = (0.02 * torch.randn(n, device=dev, generator=gen)).to(
+            torch.bfloat16)
+        d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        L = qkern.blas
+        lay = lambda r, c: L.MatrixLayout("bfloat16", r, c)
+        plan = L.BlasLt.get_matmul_plan(
+            L.GemmConfig(lay(m, k), lay(k, n), lay(m, n), lay(m, n)),
+            L.Epilogue.kBiasThenSILU)
+        args = L.MemoryArgs(a, b, None, d, bias)
+        for _ in range(3):
+            plan.execute_on_stream(None, args)
+        ms = timed_launches(torch, lambda i: plan.execute_on_stream(None, args),
+                            20)
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        out.append({"name": f"bf16 gemm+bias+silu {m}x{n}x{k}",
+                    "value": round(tf, 1), "unit": "TFLOP/s",
+                    "ms": round(ms, 4), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                    "kernel": plan.describe().split("kernel=")[-1]})
+        del a, b, d
+    # int4 batched rows (decode batch / prefill) at 12288 x 4096
+    n, k = 12288, 4096
+    sets = [make_int4(torch, dev, n, k, gen) for _ in range(8)]
+    for m in (16, 512):
+        x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        fn = lambda i: qkern.qmatvec(x, *sets[i % 8], out=y)
+        fn(0)
+        ms = timed_launches(torch, fn, 16)
+        gbs = int4_bytes(m, n, k) / (ms * 1e-3) / 1e9
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        out.append({"name": f"int4 g64 qmatvec M={m} {n}x{k}",
+                    "value": round(gbs, 1), "unit": "GB/s",
+                    "tflops": round(tf, 2), "ms": round(ms, 4),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    del sets
+    # int8 affine GEMV (C4)
+    n, k = 12288, 4096
+    sets8 = []
+    for _ in range(12):
+        codes = torch.randint(0, 256, (n, k), dtype=torch.uint8, device=dev,
+                              generator=gen)
+        s = (torch.rand(n, k // GROUP, device=dev, generator=gen) * 0.019 +
+             0.001).to(torch.bfloat16)
+        b = (0.05 * torch.randn(n, k // GROUP, device=dev, generator=gen)).to(
+            torch.bfloat16)
+        sets8.append((codes, s, b))
+    for m in (1, 8, 128):
+        x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        fn = lambda i: qkern.qmatvec(x, *sets8[i % 12], out=y,
+                                     packing=qkern.Packing.U8)
+        fn(0)
+        ms = timed_launches(torch, fn, 24)
+        gbs = int8_bytes(m, n, k) / (ms * 1e-3) / 1e9
+        out.append({"name": f"int8 affine g64 qmatvec M={m} {n}x{k}",
+                    "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    del sets8
+    # rownorm [4096, 4096]
+    for name, kind, dt, esz in [("rmsnorm bf16", 0, torch.bfloat16, 2),
+                                ("rmsnorm f32", 0, torch.float32, 4),
+                                ("softmax f32", 2, torch.float32, 4)]:
+        xs = [torch.randn(4096, 4096, device=dev, generator=gen).to(dt)
+              for _ in range(8)]
+        ys = [torch.empty_like(xs[0]) for _ in range(2)]
+        g = (1 + 0.1 * torch.randn(4096, device=dev, generator=gen))
+        gain = g if kind == 0 else None
+        fn = lambda i: qkern.rownorm(xs[i % 8], kind, eps=1e-6, gain=gain,
+                                     out=ys[i % 2])
+        fn(0)
+        ms = timed_launches(torch, fn, 32)
+        nbytes = 2 * 4096 * 4096 * esz + (4096 * 4 if kind == 0 else 0)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"name": f"{name} 4096x4096", "value": round(gbs, 1),
+                    "unit": "GB/s", "ms": round(ms, 4),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del xs, ys
+    return out
+
+
+def cpu_baseline(seconds=12.0):
+    """The oracle's C port of _matvec_int4 on a bounded sample: repeated
+    passes over the four Qwen3-8B shapes (M = 1) until `seconds` elapse."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    threads = min(16, len(os.sched_getaffinity(0)))
+    rng = np.random.default_rng(0)
+    data = []
+    for n, k in QWEN3_8B:
+        words = rng.integers(0, 2 ** 32, size=(n, k // 8), dtype=np.uint32)
+        s = O.bf16_bits(rng.uniform(0.001, 0.02, (n, k // GROUP)).astype(
+            np.float32))
+        b = O.bf16_bits((0.05 * rng.standard_normal((n, k // GROUP))).astype(
+            np.float32))
+        x = O.bf16_bits(rng.standard_normal((1, k)).astype(np.float32))
+        data.append((x, words, s, b, int4_bytes(1, n, k)))
+    O.c_matvec_int4_u32x8(*data[0][:4], threads=threads)  # warm
+    total, passes = 0, 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for x, words, s, b, nbytes in data:
+            O.c_matvec_int4_u32x8(x, words, s, b, threads=threads)
+            total += nbytes
+        passes += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(total / dt / 1e9, 2), "unit": "GB/s",
+            "cores": O.c_threads(threads), "kind": "port",
+            "sample": f"{passes} passes over the 4 Qwen3-8B int4 shapes at "
+                      f"M=1 ({dt:.1f} s), oracle/qk_oracle.c float32"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(every GPU box here has one GPU). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import qkern
+    import qkern.blas  # noqa: F401
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    rot = 3
+    sets = [[make_int4(torch, dev, n, k, gen) for (n, k) in QWEN3_8B]
+            for _ in range(rot)]
+    xs = [torch.randn(1, k, device=dev, generator=gen).to(torch.bfloat16)
+          for (n, k) in QWEN3_8B]
+    ys = [torch.empty(1, n, dtype=torch.bfloat16, device=dev)
+          for (n, k) in QWEN3_8B]
+    step_bytes = sum(int4_bytes(1, n, k) for (n, k) in QWEN3_8B)
+    per_shape_bytes = [int4_bytes(1, n, k) for (n, k) in QWEN3_8B]
+
+    def step(i, events=None):
+        ws = sets[i % rot]
+        for j in range(len(QWEN3_8B)):
+            if events is not None:
+                events[j][0].record()
+            qkern.qmatvec(xs[j], *ws[j], out=ys[j])
+            if events is not None:
+                events[j][1].record()
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)]
+           for _ in QWEN3_8B] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i, ev[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_shape_ms = [sum(ev[i][j][0].elapsed_time(ev[i][j][1])
+                        for i in range(args.steps)) / args.steps
+                    for j in range(len(QWEN3_8B))]
+    kernel_ms = sum(per_shape_ms)
+    value = step_bytes * args.steps / wall / 1e9
+    achieved = step_bytes / (kernel_ms * 1e-3) / 1e9
+    shapes = [{"n": n, "k": k, "ms": round(ms, 5),
+               "gbs": round(b / (ms * 1e-3) / 1e9, 1)}
+              for (n, k), ms, b in zip(QWEN3_8B, per_shape_ms,
+                                       per_shape_bytes)]
+    del sets
+
+    result = {
+        "metric": "int4 GEMV HBM GB/s (% of peak); bf16 GEMM TFLOP/s "
+                  "(% MFMA peak)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4xbf16->f32",
+        "data": "synthetic (uniform int4 codes, bf16 scale U(0.001,0.02) "
+                "and bias N(0,0.05) per group of 64, x ~ N(0,1) bf16)",
+        "config": {"workload": "int4 g64 u32x8 qmatvec, Qwen3-8B decode "
+                               "projections at M=1: 4096x4096, 12288x4096, "
+                               "4096x12288, 151936x4096 (one launch each "
+                               "per step, 3 rotated weight sets)",
+                   "bytes_per_step": step_bytes,
+                   "per_shape": shapes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "qmv_int4_bf16_kernel (avg over the 4 "
+                               "launches of a step)"},
+    }
+    if not args.no_secondary:
+        result["secondary"] = secondary(torch, qkern, dev, gen)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,78 @@
+// Device-side helpers shared by the gfx950 kernels: element conversion,
+// activations and wavefront reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace qk {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+
+// Element conversions. f32 -> bf16/f16 round to nearest even (the gfx950
+// conversion instructions), NaN stays NaN.
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(f16 v) { return static_cast<float>(v); }
+__device__ __forceinline__ float to_f32(bf16 v) {
+  return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, v))
+                         << 16);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v);
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ f16 from_f32<f16>(float v) {
+  return static_cast<f16>(v);
+}
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float v) {
+  return static_cast<bf16>(v);
+}
+
+// Loads element i of a float buffer whose type is chosen at run time
+// (0 f32, 1 f16, 2 bf16: the qk_dtype values).
+__device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
+  if (dtype == 2) return to_f32(static_cast<const bf16*>(p)[i]);
+  if (dtype == 1) return to_f32(static_cast<const f16*>(p)[i]);
+  return static_cast<const float*>(p)[i];
+}
+__device__ __forceinline__ void store_any(void* p, int64_t i, int dtype,
+                                          float v) {
+  if (dtype == 2)
+    static_cast<bf16*>(p)[i] = from_f32<bf16>(v);
+  else if (dtype == 1)
+    static_cast<f16*>(p)[i] = from_f32<f16>(v);
+  else
+    static_cast<float*>(p)[i] = v;
+}
+
+// cuBLASLt epilogue activations, in f32 (the reference's steel_act,
+// metal_pjrt/kernels/steel_gemm.metal:57-66): ReLU keeps NaN, GELU is the
+// tanh form, SiLU is x / (1 + exp(-x)).
+__device__ __forceinline__ float act_f32(int act, float x) {
+  if (act == 1) return x != x ? x : (x > 0.0f ? x : 0.0f);
+  if (act == 2) {
+    const float k = 0.7978845608028654f;  // sqrt(2/pi)
+    return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
+  }
+  if (act == 3) return x / (1.0f + expf(-x));
+  return x;
+}
+
+// Sum / max over the 64 lanes of a wavefront; every lane gets the result.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+}  // namespace qk

@@ -1,0 +1,107 @@
+// Internal interfaces between the C-ABI layer (qk_abi.cpp) and the kernel
+// launchers (gemm.hip, qmatvec.hip, rownorm.hip). Host-side only types; no
+// torch, no XLA.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "../../include/qkern.h"
+
+namespace qk {
+
+// ---------------------------------------------------------------------------
+// Errors (qk_abi.cpp).
+
+// Records `msg` as this thread's last error and returns `s`.
+qk_status Fail(qk_status s, const std::string& msg);
+
+// Called before every kernel launch: QK_OK, or the sticky device error.
+qk_status PreLaunch();
+
+// Called after every kernel launch: counts launches, applies the
+// QK_FAIL_LAUNCH test hook, and turns a launch error into the sticky
+// device error.
+qk_status PostLaunch(const char* kernel);
+
+int DTypeSize(int dtype);
+const char* DTypeName(int dtype);
+
+// ---------------------------------------------------------------------------
+// Dense GEMM, row-major view (the reference's mps::GemmParams,
+// metal_pjrt/blas/mps_gemm.h:29-53).
+
+struct Operand {
+  const void* ptr = nullptr;
+  int64_t ld = 0;            // elements between consecutive stored rows
+  int64_t batch_stride = 0;  // elements between batches; 0 broadcasts
+  int dtype = QK_F32;
+  bool transpose = false;    // used as op(X) = X^T
+};
+
+// For each batch b: D = act(alpha op(A) op(B) + beta C + bias[col]),
+// aux = the pre-activation value. C shares D's layout.
+struct GemmProblem {
+  int64_t m = 0, n = 0, k = 0, batch = 1;
+  float alpha = 1.f, beta = 0.f;
+  Operand a, b, d;
+  const void* c = nullptr;  // read when beta != 0 (may equal d.ptr)
+  const void* bias = nullptr;
+  void* aux = nullptr;
+  int act = 0;  // 0 none, 1 ReLU, 2 GELU (tanh), 3 SiLU
+};
+
+// Kernel choice for a problem (host only), and its name for debug output.
+struct GemmKernelChoice {
+  int family = 0;  // 0 MFMA tiles, 1 skinny (few rows / columns)
+  int bm = 0, bn = 0, bk = 0;
+  int split_k = 1;
+  std::string name;
+};
+GemmKernelChoice ChooseGemmKernel(const GemmProblem& p);
+
+// Launches the GEMM. p has been validated; m, n, batch > 0.
+qk_status LaunchGemm(const GemmProblem& p, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// Quantized matvec / dequantize (qmatvec.hip).
+
+struct QuantProblem {
+  int64_t m = 0, n = 0, k = 0;
+  int bits = 4, group = 64, packing = QK_PACK_U32X8;
+  bool has_bias = true;
+  const void* x = nullptr;
+  int x_dtype = QK_BF16;
+  const void* codes = nullptr;
+  const void* scales = nullptr;
+  int scale_dtype = QK_BF16;
+  const void* biases = nullptr;
+  int bias_dtype = QK_BF16;
+  void* y = nullptr;  // y dtype == x dtype; for dequantize, the weights
+  int y_dtype = QK_BF16;
+};
+
+qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream);
+qk_status LaunchDequantize(const QuantProblem& p, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// Row normalisation (rownorm.hip).
+
+struct RownormProblem {
+  int64_t rows = 0, n = 0;
+  int kind = QK_ROWNORM_RMS;
+  float eps = 1e-6f;
+  const void* x = nullptr;
+  void* y = nullptr;
+  int dtype = QK_F32;
+  const void* gain = nullptr;
+  int gain_dtype = QK_F32;
+  const void* beta = nullptr;
+  int beta_dtype = QK_F32;
+};
+
+qk_status LaunchRownorm(const RownormProblem& p, hipStream_t stream);
+
+}  // namespace qk

@@ -1,0 +1,491 @@
+// Group-affine int4/int8 weight-quantized matvec and dequantize for gfx950.
+//
+// Replaces the reduction fusions XLA emits for the reference's _matvec_int8 /
+// _matvec_int4 (examples/llm/qwen3.py:233-267) and its dequantize
+// (qwen3.py:199-207). Semantics, per output row o and group g:
+//   y[m, o] = sum_g ( scale[o,g] * sum_{k in g} x[m,k] q[o,k]
+//                     + bias[o,g] * sum_{k in g} x[m,k] )
+// in f32, rounded once to x's type: the reference's per-group factoring
+// (qwen3.py:246-250), which equals sum_k x[m,k] (scale*q + bias).
+//
+// The matvec is bandwidth-bound: every code byte is read once with 16-byte
+// loads, codes are widened in registers and the K reduction ends in a
+// wavefront butterfly.
+//  - A wave owns R output rows; its 64 lanes stride over the rows' 16-byte
+//    code chunks (32 int4 or 16 int8 codes), so each lane's x slice is
+//    loaded once and reused for all R rows.
+//  - bf16 x, 4-bit codes: a code pair (q_a, q_b) sharing a 32-bit word at
+//    nibbles s and s+4 becomes the bf16 pair (128+q_a, 128+q_b) with one
+//    and-or (0x4300 | q is 128 + q exactly in bf16), and v_dot2_f32_bf16
+//    multiplies it with the matching pair of x. The 128 offset is removed
+//    per group: s*sum(x(q+128)) + (b - 128 s)*sum(x).
+//  - Other types widen codes to f32 and use FMAs.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "qk_device.h"
+#include "qk_internal.h"
+
+namespace qk {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWaves = 4;  // waves per workgroup
+
+struct QmvArgs {
+  const void* x;
+  const uint8_t* codes;
+  const void* scales;
+  const void* biases;
+  void* y;
+  int m, n, k;
+  int group;
+  int sdt, bdt;  // scale / bias dtypes (qk_dtype)
+  int has_bias;
+  int row_bytes;  // bytes of codes per output row
+};
+
+__device__ __forceinline__ uint32_t PackBf16Pair(float lo, float hi) {
+  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+}
+
+// x is bf16: its values are exact in f32, so truncating back is exact.
+template <int PACK, int MT, int R>
+__global__ __launch_bounds__(kWaves * 64) void qmv_int4_bf16_kernel(
+    QmvArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int row0 = wave * R;
+  if (row0 >= a.n) return;
+  const int hg = a.group / 2;  // half group, half-split packing
+  const int chunks = a.row_bytes / 16;
+  const bf16* X = static_cast<const bf16*>(a.x);
+
+  float acc[MT][R];
+#pragma unroll
+  for (int mm = 0; mm < MT; ++mm)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[mm][r] = 0.f;
+
+  for (int c = lane; c < chunks; c += 64) {
+    // K span of the chunk: u32x8 -> 32 consecutive codes; half-split ->
+    // 16 codes at kb and 16 at kb + hg.
+    int kb, grp;
+    if (PACK == QK_PACK_U32X8) {
+      kb = c * 32;
+      grp = kb / a.group;
+    } else {
+      const int byte0 = c * 16;
+      grp = byte0 / hg;
+      kb = grp * a.group + byte0 % hg;
+    }
+    u32x4 w[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min(row0 + r, a.n - 1);
+      w[r] = *reinterpret_cast<const u32x4*>(
+          a.codes + static_cast<long long>(row) * a.row_bytes + c * 16);
+    }
+    float s[R], bb[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min(row0 + r, a.n - 1);
+      const long long gi = static_cast<long long>(row) * (a.k / a.group) + grp;
+      s[r] = load_any(a.scales, gi, a.sdt);
+      bb[r] = a.has_bias ? load_any(a.biases, gi, a.bdt) : 0.f;
+    }
+    // Code pairs (128 + q) as bf16x2, pair p = 4*i + s: nibbles s, s+4.
+    uint32_t cp[R][16];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int sh = 0; sh < 4; ++sh)
+          cp[r][4 * i + sh] = ((w[r][i] >> (4 * sh)) & 0x000F000Fu) | 0x43004300u;
+
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) {
+      if (mm >= a.m) break;
+      const bf16* xr = X + static_cast<long long>(mm) * a.k + kb;
+      float xf[32];
+      if (PACK == QK_PACK_U32X8) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const u32x4 q = *reinterpret_cast<const u32x4*>(xr + 8 * v);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            xf[8 * v + 2 * e] = __uint_as_float(q[e] << 16);
+            xf[8 * v + 2 * e + 1] = __uint_as_float(q[e] & 0xffff0000u);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int v = 0; v < 2; ++v) {
+            const u32x4 q =
+                *reinterpret_cast<const u32x4*>(xr + h * hg + 8 * v);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              xf[16 * h + 8 * v + 2 * e] = __uint_as_float(q[e] << 16);
+              xf[16 * h + 8 * v + 2 * e + 1] =
+                  __uint_as_float(q[e] & 0xffff0000u);
+            }
+          }
+      }
+      uint32_t xp[16];
+      float xs = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int sh = 0; sh < 4; ++sh) {
+          int e0, e1;
+          if (PACK == QK_PACK_U32X8) {
+            e0 = 8 * i + sh;
+            e1 = 8 * i + sh + 4;
+          } else {
+            // Nibble sh: byte 4i + sh/2 of the chunk, low (first half) for
+            // even sh; nibble sh + 4: byte 4i + 2 + sh/2.
+            e0 = ((sh & 1) ? 16 : 0) + 4 * i + (sh >> 1);
+            e1 = ((sh & 1) ? 16 : 0) + 4 * i + 2 + (sh >> 1);
+          }
+          xp[4 * i + sh] = PackBf16Pair(xf[e0], xf[e1]);
+        }
+#pragma unroll
+      for (int e = 0; e < 32; ++e) xs += xf[e];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float d = 0.f;
+#pragma unroll
+        for (int p = 0; p < 16; ++p)
+          d = __builtin_amdgcn_fdot2_f32_bf16(
+              __builtin_bit_cast(bf16x2, cp[r][p]),
+              __builtin_bit_cast(bf16x2, xp[p]), d, false);
+        acc[mm][r] += s[r] * d + (bb[r] - 128.f * s[r]) * xs;
+      }
+    }
+  }
+
+#pragma unroll
+  for (int mm = 0; mm < MT; ++mm) {
+    if (mm >= a.m) break;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(acc[mm][r]);
+      if (lane == 0 && row0 + r < a.n)
+        static_cast<bf16*>(a.y)[static_cast<long long>(mm) * a.n + row0 + r] =
+            from_f32<bf16>(v);
+    }
+  }
+}
+
+// Generic path: any x type, any packing; codes widened to f32, FMAs.
+template <typename XT, int PACK, int MT, int R>
+__global__ __launch_bounds__(kWaves * 64) void qmv_generic_kernel(QmvArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int row0 = wave * R;
+  if (row0 >= a.n) return;
+  constexpr bool kInt4 = PACK == QK_PACK_U32X8 || PACK == QK_PACK_BYTE_HALFSPLIT;
+  constexpr int kCodes = kInt4 ? 32 : 16;  // codes per 16-byte chunk
+  const int hg = a.group / 2;
+  const int chunks = a.row_bytes / 16;
+  const XT* X = static_cast<const XT*>(a.x);
+
+  float acc[MT][R];
+#pragma unroll
+  for (int mm = 0; mm < MT; ++mm)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[mm][r] = 0.f;
+
+  for (int c = lane; c < chunks; c += 64) {
+    int kb, grp;
+    if (PACK == QK_PACK_BYTE_HALFSPLIT) {
+      const int byte0 = c * 16;
+      grp = byte0 / hg;
+      kb = grp * a.group + byte0 % hg;
+    } else {
+      kb = c * kCodes;
+      grp = kb / a.group;
+    }
+    u32x4 w[R];
+    float s[R], bb[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min(row0 + r, a.n - 1);
+      w[r] = *reinterpret_cast<const u32x4*>(
+          a.codes + static_cast<long long>(row) * a.row_bytes + c * 16);
+      const long long gi = static_cast<long long>(row) * (a.k / a.group) + grp;
+      s[r] = load_any(a.scales, gi, a.sdt);
+      bb[r] = a.has_bias ? load_any(a.biases, gi, a.bdt) : 0.f;
+    }
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) {
+      if (mm >= a.m) break;
+      const XT* xr = X + static_cast<long long>(mm) * a.k + kb;
+      // xf[e]: x at chunk element e (half-split: e >= 16 is the second half).
+      float xf[kCodes];
+#pragma unroll
+      for (int e = 0; e < kCodes; ++e) {
+        int off = e;
+        if (PACK == QK_PACK_BYTE_HALFSPLIT && e >= 16) off = hg + e - 16;
+        xf[e] = to_f32(xr[off]);
+      }
+      float xs = 0.f;
+#pragma unroll
+      for (int e = 0; e < kCodes; ++e) xs += xf[e];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t word = w[r][i];
+          if (kInt4) {
+#pragma unroll
+            for (int nib = 0; nib < 8; ++nib) {
+              int e;
+              if (PACK == QK_PACK_U32X8)
+                e = 8 * i + nib;
+              else
+                e = ((nib & 1) ? 16 : 0) + 4 * i + (nib >> 1);
+              d += xf[e] * static_cast<float>((word >> (4 * nib)) & 15u);
+            }
+          } else {
+#pragma unroll
+            for (int bt = 0; bt < 4; ++bt) {
+              float q;
+              if (PACK == QK_PACK_S8_SYM)
+                q = static_cast<float>(static_cast<int8_t>(word >> (8 * bt)));
+              else
+                q = static_cast<float>((word >> (8 * bt)) & 255u);
+              d += xf[4 * i + bt] * q;
+            }
+          }
+        }
+        acc[mm][r] += s[r] * d + bb[r] * xs;
+      }
+    }
+  }
+
+#pragma unroll
+  for (int mm = 0; mm < MT; ++mm) {
+    if (mm >= a.m) break;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(acc[mm][r]);
+      if (lane == 0 && row0 + r < a.n)
+        static_cast<XT*>(a.y)[static_cast<long long>(mm) * a.n + row0 + r] =
+            from_f32<XT>(v);
+    }
+  }
+}
+
+// Dequantize: one thread per 16-byte chunk of codes.
+// w = f32(q) * f32(scale) rounded, + f32(bias) rounded, then rounded once
+// more to the output type (no fused multiply-add).
+template <int PACK, typename OT>
+__global__ void dequant_kernel(QmvArgs a, long long total_chunks) {
+  const long long t = static_cast<long long>(blockIdx.x) * blockDim.x +
+                      threadIdx.x;
+  if (t >= total_chunks) return;
+  constexpr bool kInt4 = PACK == QK_PACK_U32X8 || PACK == QK_PACK_BYTE_HALFSPLIT;
+  constexpr int kCodes = kInt4 ? 32 : 16;
+  const int cpr = a.row_bytes / 16;
+  const int row = static_cast<int>(t / cpr);
+  const int c = static_cast<int>(t % cpr);
+  const int hg = a.group / 2;
+  int kb, grp;
+  if (PACK == QK_PACK_BYTE_HALFSPLIT) {
+    const int byte0 = c * 16;
+    grp = byte0 / hg;
+    kb = grp * a.group + byte0 % hg;
+  } else {
+    kb = c * kCodes;
+    grp = kb / a.group;
+  }
+  const u32x4 w = *reinterpret_cast<const u32x4*>(
+      a.codes + static_cast<long long>(row) * a.row_bytes + c * 16);
+  const long long gi = static_cast<long long>(row) * (a.k / a.group) + grp;
+  const float s = load_any(a.scales, gi, a.sdt);
+  const float b = a.has_bias ? load_any(a.biases, gi, a.bdt) : 0.f;
+  OT* out = static_cast<OT*>(a.y) + static_cast<long long>(row) * a.k + kb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t word = w[i];
+    if (kInt4) {
+#pragma unroll
+      for (int nib = 0; nib < 8; ++nib) {
+        int off;
+        if (PACK == QK_PACK_U32X8)
+          off = 8 * i + nib;
+        else
+          off = ((nib & 1) ? hg : 0) + 4 * i + (nib >> 1);
+        const float q = static_cast<float>((word >> (4 * nib)) & 15u);
+        out[off] = from_f32<OT>(__fadd_rn(__fmul_rn(q, s), b));
+      }
+    } else {
+#pragma unroll
+      for (int bt = 0; bt < 4; ++bt) {
+        float q;
+        if (PACK == QK_PACK_S8_SYM)
+          q = static_cast<float>(static_cast<int8_t>(word >> (8 * bt)));
+        else
+          q = static_cast<float>((word >> (8 * bt)) & 255u);
+        out[4 * i + bt] = from_f32<OT>(__fadd_rn(__fmul_rn(q, s), b));
+      }
+    }
+  }
+}
+
+int RowBytes(const QuantProblem& p) {
+  return static_cast<int>(p.bits == 4 ? p.k / 2 : p.k);
+}
+
+template <typename XT, int PACK>
+qk_status LaunchGeneric(QmvArgs a, int m_total, int xsize, hipStream_t st) {
+  constexpr int MT = 4, R = 4;
+  const int waves = (a.n + R - 1) / R;
+  dim3 grid((waves + kWaves - 1) / kWaves), block(kWaves * 64);
+  const char* base_x = static_cast<const char*>(a.x);
+  char* base_y = static_cast<char*>(a.y);
+  for (int m0 = 0; m0 < m_total; m0 += MT) {
+    a.m = m_total - m0 < MT ? m_total - m0 : MT;
+    a.x = base_x + static_cast<long long>(m0) * a.k * xsize;
+    a.y = base_y + static_cast<long long>(m0) * a.n * xsize;
+    qmv_generic_kernel<XT, PACK, MT, R><<<grid, block, 0, st>>>(a);
+    if (qk_status s = PostLaunch("qmv_generic"); s != QK_OK) return s;
+  }
+  return QK_OK;
+}
+
+template <int PACK>
+qk_status LaunchInt4Bf16(QmvArgs a, int m_total, hipStream_t st) {
+  constexpr int R = 4;
+  const int waves = (a.n + R - 1) / R;
+  dim3 grid((waves + kWaves - 1) / kWaves), block(kWaves * 64);
+  const char* base_x = static_cast<const char*>(a.x);
+  char* base_y = static_cast<char*>(a.y);
+  for (int m0 = 0; m0 < m_total;) {
+    const int left = m_total - m0;
+    a.x = base_x + static_cast<long long>(m0) * a.k * 2;
+    a.y = base_y + static_cast<long long>(m0) * a.n * 2;
+    if (left == 1) {
+      a.m = 1;
+      qmv_int4_bf16_kernel<PACK, 1, R><<<grid, block, 0, st>>>(a);
+      m0 += 1;
+    } else if (left == 2) {
+      a.m = 2;
+      qmv_int4_bf16_kernel<PACK, 2, R><<<grid, block, 0, st>>>(a);
+      m0 += 2;
+    } else {
+      a.m = left < 4 ? left : 4;
+      qmv_int4_bf16_kernel<PACK, 4, R><<<grid, block, 0, st>>>(a);
+      m0 += a.m;
+    }
+    if (qk_status s = PostLaunch("qmv_int4_bf16"); s != QK_OK) return s;
+  }
+  return QK_OK;
+}
+
+QmvArgs MakeArgs(const QuantProblem& p) {
+  QmvArgs a;
+  a.x = p.x;
+  a.codes = static_cast<const uint8_t*>(p.codes);
+  a.scales = p.scales;
+  a.biases = p.biases;
+  a.y = p.y;
+  a.m = static_cast<int>(p.m);
+  a.n = static_cast<int>(p.n);
+  a.k = static_cast<int>(p.k);
+  a.group = p.group;
+  a.sdt = p.scale_dtype;
+  a.bdt = p.bias_dtype;
+  a.has_bias = p.has_bias;
+  a.row_bytes = RowBytes(p);
+  return a;
+}
+
+qk_status CheckLimits(const QuantProblem& p) {
+  if (p.n > 0x7fffffff || p.k > 0x7fffffff || p.m > 0x7fffffff ||
+      p.n * (p.k / p.group) > (int64_t{1} << 40)) {
+    return Fail(QK_UNIMPLEMENTED, "qkern: quantized matrix too large");
+  }
+  if (reinterpret_cast<uintptr_t>(p.codes) % 16 != 0) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: quantized codes must be 16-byte aligned");
+  }
+  return QK_OK;
+}
+
+}  // namespace
+
+qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream) {
+  if (qk_status s = CheckLimits(p); s != QK_OK) return s;
+  if (reinterpret_cast<uintptr_t>(p.x) % 16 != 0) {
+    return Fail(QK_INVALID_ARGUMENT, "qkern: qmatvec x must be 16-byte aligned");
+  }
+  QmvArgs a = MakeArgs(p);
+  const int m = static_cast<int>(p.m);
+  if (p.x_dtype == QK_BF16 && p.packing == QK_PACK_U32X8)
+    return LaunchInt4Bf16<QK_PACK_U32X8>(a, m, stream);
+  if (p.x_dtype == QK_BF16 && p.packing == QK_PACK_BYTE_HALFSPLIT)
+    return LaunchInt4Bf16<QK_PACK_BYTE_HALFSPLIT>(a, m, stream);
+#define QK_GENERIC(XT, XS)                                                 \
+  switch (p.packing) {                                                     \
+    case QK_PACK_U32X8:                                                    \
+      return LaunchGeneric<XT, QK_PACK_U32X8>(a, m, XS, stream);           \
+    case QK_PACK_BYTE_HALFSPLIT:                                           \
+      return LaunchGeneric<XT, QK_PACK_BYTE_HALFSPLIT>(a, m, XS, stream);  \
+    case QK_PACK_U8:                                                       \
+      return LaunchGeneric<XT, QK_PACK_U8>(a, m, XS, stream);              \
+    default:                                                               \
+      return LaunchGeneric<XT, QK_PACK_S8_SYM>(a, m, XS, stream);          \
+  }
+  if (p.x_dtype == QK_BF16) {
+    QK_GENERIC(bf16, 2)
+  } else if (p.x_dtype == QK_F16) {
+    QK_GENERIC(f16, 2)
+  } else {
+    QK_GENERIC(float, 4)
+  }
+#undef QK_GENERIC
+}
+
+qk_status LaunchDequantize(const QuantProblem& p, hipStream_t stream) {
+  if (qk_status s = CheckLimits(p); s != QK_OK) return s;
+  QmvArgs a = MakeArgs(p);
+  const long long chunks = p.n * (a.row_bytes / 16);
+  dim3 block(256), grid(static_cast<unsigned>((chunks + 255) / 256));
+#define QK_DQ(OT)                                                              \
+  switch (p.packing) {                                                         \
+    case QK_PACK_U32X8:                                                        \
+      dequant_kernel<QK_PACK_U32X8, OT><<<grid, block, 0, stream>>>(a, chunks); \
+      break;                                                                   \
+    case QK_PACK_BYTE_HALFSPLIT:                                               \
+      dequant_kernel<QK_PACK_BYTE_HALFSPLIT, OT>                               \
+          <<<grid, block, 0, stream>>>(a, chunks);                             \
+      break;                                                                   \
+    case QK_PACK_U8:                                                           \
+      dequant_kernel<QK_PACK_U8, OT><<<grid, block, 0, stream>>>(a, chunks);    \
+      break;                                                                   \
+    default:                                                                   \
+      dequant_kernel<QK_PACK_S8_SYM, OT><<<grid, block, 0, stream>>>(a, chunks); \
+  }
+  if (p.y_dtype == QK_BF16) {
+    QK_DQ(bf16)
+  } else if (p.y_dtype == QK_F16) {
+    QK_DQ(f16)
+  } else {
+    QK_DQ(float)
+  }
+#undef QK_DQ
+  return PostLaunch("dequantize");
+}
+
+}  // namespace qk

@@ -1,0 +1,28 @@
+"""qkern: the MI355X (gfx950) hot path of the metal-pjrt-plugin JAX plugin.
+
+Three kernel families behind a C ABI (include/qkern.h, libqkern.so):
+  - blas:  BlasLt matmul plans, f32/f16/bf16 with the cuBLASLt epilogue;
+  - ffi:   qk$qmatvec / qk$dequantize (int4 / int8 group-affine weights)
+           and qk$rownorm (RMSNorm, LayerNorm, softmax);
+  - quant: host-side quantizers and packers for the weight formats.
+Every compute call runs a HIP kernel; there is no CPU fallback.
+"""
+
+from ._lib import QkError, lib  # noqa: F401
+from .blas import (BlasLt, Epilogue, GemmConfig, MatmulPlan,  # noqa: F401
+                   MatrixLayout, MemoryArgs, Order, matmul)
+from .ffi import (Packing, RownormKind, dequantize, layer_norm,  # noqa: F401
+                  qmatvec, rms_norm, rownorm, softmax)
+
+
+def version():
+    return lib().qk_version().decode()
+
+
+def device_error():
+    """0, or the sticky device error code."""
+    return lib().qk_device_error()
+
+
+def reset_device_error():
+    lib().qk_reset_device_error()

@@ -1,0 +1,127 @@
+"""Typed-FFI style targets: qk$qmatvec, qk$dequantize, qk$rownorm.
+
+The reference has no custom-call target for these (XLA fuses the JAX code
+of examples/llm/qwen3.py into reduction kernels). They follow the
+reference's convention for a new target (metal_pjrt/ffi/scan_ffi.cc:
+112-133): operands then results as FFI AnyBuffers (data, element type,
+dimensions), then attributes. Buffers here are torch device tensors.
+"""
+
+import ctypes
+import enum
+
+import torch
+
+from . import _lib
+from ._lib import check, lib
+from .blas import stream_handle
+
+
+class Packing(enum.IntEnum):
+    U32X8 = 0            # 4-bit, 8 codes per uint32 along K
+    BYTE_HALFSPLIT = 1   # 4-bit, qwen3.quantize_int4's byte layout
+    U8 = 2               # 8-bit unsigned affine
+    S8_SYM = 3           # 8-bit signed symmetric (qwen3.quantize_int8)
+
+
+class RownormKind(enum.IntEnum):
+    RMS = 0
+    LAYER = 1
+    SOFTMAX = 2
+
+
+_TORCH_DT = {
+    torch.float32: _lib.F32, torch.float16: _lib.F16,
+    torch.bfloat16: _lib.BF16, torch.uint8: _lib.U8, torch.int8: _lib.S8,
+    torch.int32: _lib.U32, torch.uint32: _lib.U32,
+}
+
+
+def any_buffer(t):
+    """An FFI AnyBuffer descriptor of a contiguous torch tensor (or None)."""
+    if t is None:
+        return None
+    if not t.is_contiguous():
+        raise ValueError("qkern buffers must be contiguous")
+    if t.dtype not in _TORCH_DT:
+        raise ValueError(f"unsupported buffer dtype {t.dtype}")
+    if t.dim() > _lib.MAX_RANK or t.dim() == 0:
+        raise ValueError(f"buffer rank {t.dim()} not in 1..{_lib.MAX_RANK}")
+    b = _lib.BufferC()
+    b.data = t.data_ptr()
+    b.dtype = _TORCH_DT[t.dtype]
+    b.rank = t.dim()
+    for i, s in enumerate(t.shape):
+        b.dims[i] = s
+    return b
+
+
+def _ref(b):
+    return ctypes.byref(b) if b is not None else None
+
+
+def _attrs(packing, group_size, has_bias):
+    packing = Packing(packing)
+    bits = 4 if packing in (Packing.U32X8, Packing.BYTE_HALFSPLIT) else 8
+    return _lib.QuantAttrsC(bits, group_size, int(packing), int(bool(has_bias)))
+
+
+def qmatvec(x, codes, scales, biases=None, *, packing=Packing.U32X8,
+            group_size=64, out=None, stream=None):
+    """qk$qmatvec: y[..., o] = sum_k x[..., k] * (scale*q + bias)[o, k].
+
+    x [..., K] f32/f16/bf16; codes per `packing`; scales/biases [N, K/g].
+    Returns y [..., N] in x's dtype.
+    """
+    n = codes.shape[0]
+    if out is None:
+        out = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=x.device)
+    bx, bc, bs, bb, by = (any_buffer(t) for t in (x, codes, scales, biases,
+                                                   out))
+    attrs = _attrs(packing, group_size, biases is not None)
+    check(lib().qk_qmatvec(stream_handle(stream), _ref(bx), _ref(bc),
+                           _ref(bs), _ref(bb), _ref(by), ctypes.byref(attrs)))
+    return out
+
+
+def dequantize(codes, scales, biases=None, *, k, packing=Packing.U32X8,
+               group_size=64, dtype=torch.bfloat16, out=None, stream=None):
+    """qk$dequantize: the [N, K] weights, each f32(q)*f32(s) + f32(b)
+    rounded once to `dtype`."""
+    n = codes.shape[0]
+    if out is None:
+        out = torch.empty(n, k, dtype=dtype, device=codes.device)
+    bc, bs, bb, bw = (any_buffer(t) for t in (codes, scales, biases, out))
+    attrs = _attrs(packing, group_size, biases is not None)
+    check(lib().qk_dequantize(stream_handle(stream), _ref(bc), _ref(bs),
+                              _ref(bb), _ref(bw), ctypes.byref(attrs)))
+    return out
+
+
+def rownorm(x, kind, *, eps=1e-6, gain=None, beta=None, out=None,
+            stream=None):
+    """qk$rownorm over the last dimension of x (RMS, LAYER or SOFTMAX)."""
+    if out is None:
+        out = torch.empty_like(x)
+    bx, bg, bb, by = (any_buffer(t) for t in (x, gain, beta, out))
+    attrs = _lib.RownormAttrsC(int(RownormKind(kind)), float(eps),
+                               int(gain is not None), int(beta is not None))
+    check(lib().qk_rownorm(stream_handle(stream), _ref(bx), _ref(bg),
+                           _ref(bb), _ref(by), ctypes.byref(attrs)))
+    return out
+
+
+def rms_norm(x, w, eps):
+    """qwen3.rms_norm (examples/llm/qwen3.py:294-297) on the GPU."""
+    return rownorm(x, RownormKind.RMS, eps=eps, gain=w)
+
+
+def softmax(x):
+    """jax.nn.softmax(x, axis=-1) on the GPU."""
+    return rownorm(x, RownormKind.SOFTMAX)
+
+
+def layer_norm(x, eps=1e-5, gain=None, beta=None):
+    """(x - mean) / sqrt(var + eps) [* gain + beta] over the last axis
+    (bench/jax_bench.py:44-46 without the affine terms)."""
+    return rownorm(x, RownormKind.LAYER, eps=eps, gain=gain, beta=beta)

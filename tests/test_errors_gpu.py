@@ -1,0 +1,56 @@
+"""Failure handling (reference: tests/test_gpu_errors.py, the sticky device
+error of metal_pjrt/runtime/metal_runtime.h:43-53 and the
+METAL_PJRT_FAIL_COMMAND_BUFFER hook). The failure is injected on the host
+(QK_FAIL_LAUNCH=n marks the n-th launch failed after it was issued), so
+every kernel still runs to completion: a failed call raises, later calls
+keep raising until the error is reset, and values are never silently
+wrong.
+"""
+
+import os
+
+import pytest
+import torch
+
+import qkern
+from qkern import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def test_injected_launch_failure_is_sticky(dev):
+    x = torch.randn(4, 256, device=dev)
+    try:
+        os.environ["QK_FAIL_LAUNCH"] = "2"
+        qkern.reset_device_error()  # re-reads the environment
+        y1 = qkern.softmax(x)  # launch 1: fine
+        torch.cuda.synchronize()
+        assert torch.allclose(y1.sum(-1), torch.ones(4, device=dev))
+        with pytest.raises(qkern.QkError) as e:
+            qkern.softmax(x)  # launch 2: injected failure
+        assert e.value.status == _lib.INTERNAL
+        assert "QK_FAIL_LAUNCH" in e.value.message
+        assert qkern.device_error() == _lib.INTERNAL
+        with pytest.raises(qkern.QkError) as e:  # sticky, other target too
+            qkern.matmul(x, x.T.contiguous())
+        assert "earlier GPU launch failed" in e.value.message
+    finally:
+        os.environ.pop("QK_FAIL_LAUNCH", None)
+        qkern.reset_device_error()
+    torch.cuda.synchronize()
+    assert qkern.device_error() == 0
+    y = qkern.softmax(x)
+    torch.cuda.synchronize()
+    assert torch.allclose(y, torch.softmax(x, -1), atol=1e-6)
+
+
+def test_host_argument_errors_are_not_sticky(dev):
+    x = torch.randn(2, 100, device=dev, dtype=torch.bfloat16)
+    words = torch.zeros(8, 32, dtype=torch.int32, device=dev)
+    s = torch.zeros(8, 4, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(qkern.QkError):
+        qkern.qmatvec(x, words, s, s)
+    assert qkern.device_error() == 0
+    y = qkern.rms_norm(x, None, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()

@@ -1,0 +1,279 @@
+"""GPU parity of the BlasLt GEMM (gemm.hip) against the float64 oracle.
+
+Cases follow the reference's device tests:
+  - metal_pjrt/blas/steel_gemm_test.cc:225-330 (transposes, unaligned
+    shapes, dtype/output combinations, alpha/beta, K = 0, batched/strided/
+    broadcast, leading-dimension padding left untouched, tile configs,
+    K = 4096), with its tolerance
+      |got - want| <= eps(out)*|want| + (1e-5 + 1e-6 K)*sum|a b| + 1e-6;
+  - metal_pjrt/blas/metal_blas_lt_test.cc:96-330 (all 12 epilogues x
+    f32/f16/bf16 x row/column-major output x {5x7x3, 64x96x36}, batch 2, on
+    exact-product inputs), tolerance tol*(1 + |want|), tol = 1e-5 / 4e-3 /
+    2e-2 for f32 / f16 / bf16;
+  - f32 1024^3 within 1e-5 relative Frobenius error of
+    the float64 product; bf16 + bias + SiLU at the Qwen3-8B MLP shapes
+    within 1e-2 relative error.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import qkern
+from qkern.blas import (BlasLt, Epilogue, GemmConfig, MatrixLayout,
+                        MemoryArgs, Order)
+from helpers import EPS, StoredMatrix, from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(dev, m, n, k, batch=1, tin="bfloat16", tout=None, ta=False,
+             tb=False, alpha=1.0, beta=0.0, pad=0, broadcast_b=False,
+             epilogue=Epilogue.kDefault, separate_c=False, seed=1234):
+    tout = tout or tin
+    rng = np.random.default_rng(seed)
+    A = StoredMatrix(rng, k, m, pad, batch, tin) if ta else \
+        StoredMatrix(rng, m, k, pad, batch, tin)
+    B = StoredMatrix(rng, n, k, pad, batch, tin, broadcast_b) if tb else \
+        StoredMatrix(rng, k, n, pad, batch, tin, broadcast_b)
+    D = StoredMatrix(rng, m, n, pad, batch, tout)
+    bias_v = O.round_to(rng.uniform(-1, 1, n), tout)
+    has_bias, act, has_aux = O.EPILOGUES[int(epilogue)]
+
+    order = lambda t: Order.kColumnMajor if t else Order.kRowMajor
+    lhs = MatrixLayout(tin, m, k, order(ta), batch, A.ld, A.stride)
+    rhs = MatrixLayout(tin, k, n, order(tb), 1 if broadcast_b else batch, B.ld,
+                       B.stride)
+    out = MatrixLayout(tout, m, n, Order.kRowMajor, batch, D.ld, D.stride)
+    plan = BlasLt.get_matmul_plan(GemmConfig(lhs, rhs, out, out, alpha, beta),
+                                  epilogue)
+    da, db = to_dev(A.values, tin, dev), to_dev(B.values, tin, dev)
+    dd = to_dev(D.values, tout, dev)
+    dc = to_dev(D.values, tout, dev) if separate_c else None
+    if separate_c:
+        dd = to_dev(O.round_to(rng.uniform(-1, 1, D.elems), tout), tout, dev)
+    dbias = to_dev(bias_v, tout, dev) if has_bias else None
+    daux = torch.full_like(dd, 7.0) if has_aux else None
+    plan.execute_on_stream(None, MemoryArgs(da, db, dc, dd, dbias, daux))
+    torch.cuda.synchronize()
+    got = from_dev(dd)
+    aux = from_dev(daux) if has_aux else None
+
+    bad = []
+    for bt in range(batch):
+        a = A.matrix(bt).T if ta else A.matrix(bt)
+        b = B.matrix(bt if not broadcast_b else 0)
+        b = b.T if tb else b
+        c0 = D.matrix(bt)
+        want_act, want = O.gemm_ref(a, b, c0, bias_v if has_bias else None,
+                                    alpha, beta, act)
+        mag = abs(alpha) * (np.abs(a) @ np.abs(b)) + abs(beta) * np.abs(c0)
+        if has_bias:
+            mag = mag + np.abs(bias_v)
+        tol = EPS[tout] * np.abs(want) + (1e-5 + 1e-6 * k) * mag + 1e-6
+        gm = np.zeros((m, n))
+        for i in range(m):
+            gm[i] = got[bt * D.stride + i * D.ld: bt * D.stride + i * D.ld + n]
+        # the activation is at most 1.13-Lipschitz (GELU), 1.1 (SiLU)
+        tol_act = EPS[tout] * np.abs(want_act) + 1.2 * tol
+        err = np.abs(gm - want_act)
+        nan_ok = np.isnan(gm) & np.isnan(want_act)
+        if not np.all((err <= tol_act) | nan_ok):
+            i, j = np.unravel_index(np.argmax(err - tol_act), err.shape)
+            bad.append(f"batch {bt} ({i},{j}): got {gm[i, j]} want "
+                       f"{want_act[i, j]}")
+        if has_aux:
+            am = np.array([aux[bt * D.stride + i * D.ld:
+                               bt * D.stride + i * D.ld + n] for i in range(m)])
+            if not np.all(np.abs(am - want) <= tol):
+                bad.append(f"aux batch {bt}")
+        # padding between rows untouched (steel_gemm_test.cc:203-211)
+        for i in range(m - 1):
+            s = bt * D.stride + i * D.ld
+            if not separate_c and not np.array_equal(
+                    got[s + n:s + D.ld], D.values[s + n:s + D.ld]):
+                bad.append(f"padding clobbered in row {i}")
+    assert not bad, (plan.describe(), bad[:5])
+    return plan
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_aligned_all_transposes(dev, ta, tb):
+    run_case(dev, 128, 128, 64, ta=ta, tb=tb)
+
+
+UNALIGNED = [(1, 1, 1), (3, 5, 7), (65, 63, 17), (100, 37, 50), (33, 129, 8),
+             (130, 70, 300), (7, 200, 1), (64, 64, 15), (257, 31, 33)]
+
+
+@pytest.mark.parametrize("shape", UNALIGNED)
+@pytest.mark.parametrize("tin", ["bfloat16", "float32"])
+def test_unaligned_shapes(dev, shape, tin):
+    for ta in (False, True):
+        for tb in (False, True):
+            run_case(dev, *shape, tin=tin, ta=ta, tb=tb)
+
+
+@pytest.mark.parametrize("combo", [("bfloat16", "bfloat16"),
+                                   ("bfloat16", "float32"),
+                                   ("float16", "float16"),
+                                   ("float16", "float32"),
+                                   ("float32", "float32")])
+def test_dtypes_and_outputs(dev, combo):
+    for m in (64, 77):
+        run_case(dev, m, 96, 40, tin=combo[0], tout=combo[1], tb=True)
+
+
+def test_alpha_beta(dev):
+    for tout in ("bfloat16", "float32"):
+        for alpha, beta in ((2.0, 0.0), (1.0, 1.0), (0.5, -1.5)):
+            for m in (64, 45):
+                run_case(dev, m, 64, 32, tout=tout, alpha=alpha, beta=beta)
+    # distinct C buffer (D = alpha AB + beta C, C not overwritten)
+    run_case(dev, 70, 33, 20, alpha=1.0, beta=0.5, separate_c=True)
+    run_case(dev, 70, 33, 20, tin="float32", alpha=1.0, beta=-2.0,
+             separate_c=True)
+
+
+def test_zero_k_gives_beta_c(dev):
+    for tin in ("bfloat16", "float32"):
+        run_case(dev, 20, 30, 0, tin=tin, beta=0.5)
+        run_case(dev, 20, 30, 0, tin=tin)
+        run_case(dev, 20, 30, 0, tin=tin, epilogue=Epilogue.kBiasThenSILU)
+
+
+def test_batched_strided_and_broadcast(dev):
+    run_case(dev, 50, 70, 30, batch=5, pad=3)
+    run_case(dev, 50, 70, 30, batch=5, pad=3, broadcast_b=True, tb=True)
+    run_case(dev, 128, 128, 64, batch=16, beta=1.0)
+    run_case(dev, 50, 70, 30, batch=3, pad=2, tin="float32", ta=True)
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_leading_dim_padding(dev, ta, tb):
+    run_case(dev, 64, 64, 48, pad=5, ta=ta, tb=tb)
+    run_case(dev, 64, 64, 48, pad=5, ta=ta, tb=tb, tin="float16")
+
+
+@pytest.mark.parametrize("shape,kernel", [
+    ((97, 160, 72), "64x64"),
+    ((1536, 1536, 72), "128x128"),
+    ((3584, 3584, 40), "256x256"),
+])
+def test_all_tile_configs(dev, shape, kernel):
+    for ta in (False, True):
+        for tb in (False, True):
+            m, n, k = shape
+            if m > 1000 and (ta or tb) and (ta != tb):
+                continue  # keep the large cases to NN and TT
+            plan = run_case(dev, m, n, k, ta=ta, tb=tb,
+                            beta=1.0 if m % 2 else 0.0)
+            assert kernel in plan.describe()
+    plan = run_case(dev, 2048, 2048, 40, tin="float32")
+    assert "128x128" in plan.describe()
+
+
+def test_large_k(dev):
+    run_case(dev, 64, 64, 4096, tout="float32")
+    run_case(dev, 64, 64, 4096, tin="float32")
+
+
+# ---------------------------------------------------------------------------
+# metal_blas_lt_test.cc: every epilogue x dtype x output order x shape.
+
+
+def exact_inputs(batch, m, n, k, bias_len):
+    a = np.array([((i * 7) % 9) * 0.25 - 1.0 for i in range(batch * m * k)])
+    b = np.array([((i * 5) % 11) * 0.25 - 1.25 for i in range(batch * k * n)])
+    bias = np.array([0.5 * i - 1.0 for i in range(bias_len)])
+    return a, b, bias
+
+
+@pytest.mark.parametrize("epilogue", list(Epilogue))
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("order", [Order.kRowMajor, Order.kColumnMajor])
+@pytest.mark.parametrize("shape", [(5, 7, 3), (64, 96, 36)])
+def test_epilogues_like_reference(dev, epilogue, dtype, order, shape):
+    m, n, k = shape
+    batch = 2
+    bias_len = n if order == Order.kRowMajor else m
+    a, b, bias = exact_inputs(batch, m, n, k, bias_len)
+    has_bias, act, has_aux = O.EPILOGUES[int(epilogue)]
+    out_layout = MatrixLayout(dtype, m, n, order, batch)
+    cfg = GemmConfig(MatrixLayout(dtype, m, k, Order.kRowMajor, batch),
+                     MatrixLayout(dtype, k, n, Order.kRowMajor, batch),
+                     out_layout, out_layout)
+    plan = BlasLt.get_matmul_plan(cfg, epilogue)
+    da, db = to_dev(a, dtype, dev), to_dev(b, dtype, dev)
+    dbias = to_dev(O.round_to(bias, dtype), dtype, dev)
+    dd = torch.zeros(batch * m * n, dtype=da.dtype, device=dev)
+    daux = torch.zeros_like(dd)
+    plan.execute_on_stream(None, MemoryArgs(da, db, None, dd,
+                                            dbias if has_bias else None,
+                                            daux if has_aux else None))
+    torch.cuda.synchronize()
+    got, got_aux = from_dev(dd), from_dev(daux)
+    tol = {"float32": 1e-5, "float16": 4e-3, "bfloat16": 2e-2}[dtype]
+    ar, br = O.round_to(a, dtype), O.round_to(b, dtype)
+    for bt in range(batch):
+        A = ar[bt * m * k:(bt + 1) * m * k].reshape(m, k)
+        B = br[bt * k * n:(bt + 1) * k * n].reshape(k, n)
+        pre = A @ B
+        if has_bias:
+            bv = O.round_to(bias, dtype)
+            pre = pre + (bv[None, :] if order == Order.kRowMajor else
+                         bv[:, None])
+        want = O.ACTS[act](pre)
+        g = got[bt * m * n:(bt + 1) * m * n]
+        g = g.reshape(m, n) if order == Order.kRowMajor else g.reshape(n, m).T
+        assert np.all(np.abs(g - want) <= tol * (1 + np.abs(want))), \
+            (plan.describe(), np.max(np.abs(g - want)))
+        if has_aux:
+            ga = got_aux[bt * m * n:(bt + 1) * m * n]
+            ga = ga.reshape(m, n) if order == Order.kRowMajor else \
+                ga.reshape(n, m).T
+            assert np.all(np.abs(ga - pre) <= tol * (1 + np.abs(pre)))
+
+
+# ---------------------------------------------------------------------------
+# BASELINE configs at full size.
+
+
+def test_config_f32_1024_cubed(dev):
+    a, b = O.config_gemm_f32(0, 1024)
+    da, db = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+    d = qkern.matmul(da, db)
+    torch.cuda.synchronize()
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    err = O.rel_fro(d.cpu().numpy(), want)
+    assert err <= 1e-5, err
+
+
+@pytest.mark.parametrize("shape", [(4096, 4096, 4096), (2048, 12288, 4096),
+                                   (2048, 4096, 12288)])
+def test_config_bf16_bias_silu(dev, shape):
+    m, n, k = shape
+    g = torch.Generator(device="cpu").manual_seed(0)
+    a = (torch.randn(m, k, generator=g) / k ** 0.5).to(torch.bfloat16)
+    b = (torch.randn(k, n, generator=g) / k ** 0.5).to(torch.bfloat16)
+    bias = (0.02 * torch.randn(n, generator=g)).to(torch.bfloat16)
+    d = qkern.matmul(a.to(dev), b.to(dev), bias.to(dev),
+                     epilogue=Epilogue.kBiasThenSILU)
+    torch.cuda.synchronize()
+    # float64 reference on a sample of rows (full product on the CPU in
+    # float64 is 137-206 GFLOP)
+    rows = np.r_[0:64, m - 64:m]
+    a64 = a.float().numpy().astype(np.float64)[rows]
+    want, _ = O.gemm_ref(a64, b.float().numpy(), None,
+                         bias.float().numpy(), act=3)
+    got = d[rows].float().cpu().numpy()
+    err = O.rel_fro(got, want)
+    assert err <= 1e-2, err
+    # and all rows against torch's own bf16 GEMM (library, fp32 accumulate)
+    ref = torch.nn.functional.silu(a.to(dev).float() @ b.to(dev).float() +
+                                   bias.to(dev).float())
+    err_all = (d.float() - ref).norm() / ref.norm()
+    assert float(err_all) <= 1e-2

@@ -1,0 +1,244 @@
+"""GPU parity of qk$qmatvec and qk$dequantize (qmatvec.hip).
+
+Dequantized weights must match the oracle bit-exactly (canonical rounding
+bf16/f16/f32 of f32(f32(q)*f32(s)) + f32(b)). The matvec must be within
+1e-2 relative error (Frobenius over the output, and elementwise against
+1e-2*|want| + 1e-3*sum_k |x w|) of the float64 product of the dequantized
+float32 weights. At the BASELINE.json shapes the reference is the oracle's
+C port (float32, the reference's per-group factoring).
+
+The reference ships no test for its quantized path (its only check is a
+KL-divergence run that downloads Qwen3 weights), so the cases here cover
+the layouts (both 4-bit packings, affine u8, symmetric s8), the activation
+types, group sizes, ragged N, single-group K, and M from 1 (decode) to 512
+(prefill).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import qkern
+from qkern import quant
+from qkern.ffi import Packing
+from helpers import TORCH
+
+pytestmark = pytest.mark.gpu
+
+
+def make_weights(rng, n, k, packing, group, sdt="bfloat16", has_bias=True):
+    """Random codes + scale/offset; returns (device codes, device s, device
+    b or None, float32 dequantized weights [N, K])."""
+    bits = 4 if packing in (Packing.U32X8, Packing.BYTE_HALFSPLIT) else 8
+    if packing == Packing.S8_SYM:
+        codes = rng.integers(-127, 128, size=(n, k)).astype(np.int8)
+        has_bias = False
+    else:
+        codes = rng.integers(0, 16 if bits == 4 else 256, size=(n, k)).astype(
+            np.uint8)
+    s = O.round_to(rng.uniform(0.001, 0.02, (n, k // group)), sdt).astype(
+        np.float32)
+    b = O.round_to(0.05 * rng.standard_normal((n, k // group)), sdt).astype(
+        np.float32) if has_bias else None
+    w = O.dequantize_f32(codes.reshape(n, -1, group).astype(np.float32),
+                         s[..., None], None if b is None else b[..., None])
+    if packing == Packing.U32X8:
+        dc = torch.from_numpy(quant.pack_u32x8(codes).view(np.int32))
+    elif packing == Packing.BYTE_HALFSPLIT:
+        dc = torch.from_numpy(quant.pack_halfsplit(codes, group))
+    else:
+        dc = torch.from_numpy(codes)
+    ds = torch.from_numpy(s).to(TORCH[sdt])
+    db = None if b is None else torch.from_numpy(b).to(TORCH[sdt])
+    return dc, ds, db, w, codes, s, b
+
+
+def check_matvec(got, x, w, tol=1e-2):
+    want = O.matvec_f64(x, w)
+    mag = np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T
+    err = np.abs(got - want)
+    assert O.rel_fro(got, want) <= tol
+    bound = tol * np.abs(want) + 1e-3 * mag
+    assert np.all(err <= bound), float(np.max(err - bound))
+
+
+CASES = [
+    # (m, n, k, group)
+    (1, 1, 64, 64), (1, 13, 256, 64), (2, 64, 512, 32), (3, 257, 256, 128),
+    (4, 100, 4096, 64), (5, 37, 1024, 64), (8, 64, 2048, 64),
+    (16, 48, 512, 64), (33, 20, 256, 64), (128, 24, 512, 64),
+]
+
+
+@pytest.mark.parametrize("packing", list(Packing))
+@pytest.mark.parametrize("xdt", ["bfloat16", "float16", "float32"])
+def test_qmatvec_small(dev, packing, xdt):
+    rng = np.random.default_rng(int(packing) * 10 + len(xdt))
+    for (m, n, k, group) in CASES:
+        if packing == Packing.BYTE_HALFSPLIT and group < 32:
+            continue
+        dc, ds, db, w, *_ = make_weights(rng, n, k, packing, group)
+        x = O.round_to(rng.standard_normal((m, k)), xdt).astype(np.float32)
+        dx = torch.from_numpy(x).to(TORCH[xdt]).to(dev)
+        y = qkern.qmatvec(dx, dc.to(dev), ds.to(dev),
+                          None if db is None else db.to(dev), packing=packing,
+                          group_size=group)
+        torch.cuda.synchronize()
+        assert y.shape == (m, n) and y.dtype == TORCH[xdt]
+        check_matvec(y.float().cpu().numpy().astype(np.float64), x, w)
+
+
+def test_qmatvec_leading_dims_and_no_bias(dev):
+    rng = np.random.default_rng(5)
+    dc, ds, _, w, *_ = make_weights(rng, 40, 256, Packing.U32X8, 64,
+                                    has_bias=False)
+    x = O.round_to(rng.standard_normal((2, 3, 256)), "bfloat16").astype(
+        np.float32)
+    y = qkern.qmatvec(torch.from_numpy(x).to(torch.bfloat16).to(dev),
+                      dc.to(dev), ds.to(dev), None)
+    torch.cuda.synchronize()
+    assert y.shape == (2, 3, 40)
+    check_matvec(y.float().cpu().numpy().reshape(6, 40), x.reshape(6, 256), w)
+
+
+def test_qmatvec_f32_scales(dev):
+    rng = np.random.default_rng(6)
+    dc, ds, db, w, *_ = make_weights(rng, 33, 512, Packing.U8, 64,
+                                     sdt="float32")
+    x = O.round_to(rng.standard_normal((3, 512)), "bfloat16").astype(
+        np.float32)
+    y = qkern.qmatvec(torch.from_numpy(x).to(torch.bfloat16).to(dev),
+                      dc.to(dev), ds.to(dev), db.to(dev), packing=Packing.U8)
+    torch.cuda.synchronize()
+    check_matvec(y.float().cpu().numpy(), x, w)
+
+
+def test_qmatvec_reference_quantizer_end_to_end(dev):
+    # The reference's own pipeline: quantize_int4 -> half-split bytes, s/b
+    # cast to bf16 by put() (qwen3.py:113-128), then _matvec_int4.
+    rng = np.random.default_rng(7)
+    wf = rng.standard_normal((96, 1024)).astype(np.float32) * 0.05
+    codes, s, b = quant.quantize_int4(wf)
+    sb, bb = O.bf16_round(s), O.bf16_round(b)
+    packed = quant.pack_halfsplit(codes)
+    x = O.bf16_round(rng.standard_normal((1, 1024)).astype(np.float32))
+    y = qkern.qmatvec(torch.from_numpy(x).to(torch.bfloat16).to(dev),
+                      torch.from_numpy(packed).to(dev),
+                      torch.from_numpy(sb).to(torch.bfloat16).to(dev),
+                      torch.from_numpy(bb).to(torch.bfloat16).to(dev),
+                      packing=Packing.BYTE_HALFSPLIT)
+    torch.cuda.synchronize()
+    want_ref_form = O.matvec_int4_reference_form(
+        x, packed.reshape(96, -1, 32), sb.reshape(96, -1, 1),
+        bb.reshape(96, -1, 1))
+    got = y.float().cpu().numpy()
+    assert O.rel_fro(got, want_ref_form) <= 1e-2
+    # symmetric int8 path of the same weights
+    q8, s8 = quant.quantize_int8(wf)
+    s8b = O.bf16_round(s8)
+    y8 = qkern.qmatvec(torch.from_numpy(x).to(torch.bfloat16).to(dev),
+                       torch.from_numpy(q8).to(dev),
+                       torch.from_numpy(s8b).to(torch.bfloat16).to(dev), None,
+                       packing=Packing.S8_SYM)
+    torch.cuda.synchronize()
+    want8 = O.matvec_int8_reference_form(x, q8.reshape(96, -1, 64),
+                                         s8b.reshape(96, -1, 1))
+    assert O.rel_fro(y8.float().cpu().numpy(), want8) <= 1e-2
+
+
+@pytest.mark.parametrize("packing", list(Packing))
+@pytest.mark.parametrize("odt", ["bfloat16", "float16", "float32"])
+def test_dequantize_bit_exact(dev, packing, odt):
+    rng = np.random.default_rng(8)
+    for (n, k, group) in [(7, 64, 64), (33, 512, 32), (16, 1024, 128)]:
+        dc, ds, db, w, codes, s, b = make_weights(rng, n, k, packing, group)
+        out = qkern.dequantize(dc.to(dev), ds.to(dev),
+                               None if db is None else db.to(dev), k=k,
+                               packing=packing, group_size=group,
+                               dtype=TORCH[odt])
+        torch.cuda.synchronize()
+        if odt == "bfloat16":
+            want = O.bf16_bits(w)
+            got = out.view(torch.int16).cpu().numpy().view(np.uint16)
+        elif odt == "float16":
+            want = w.astype(np.float16).view(np.uint16)
+            got = out.view(torch.int16).cpu().numpy().view(np.uint16)
+        else:
+            want = w.view(np.uint32)
+            got = out.view(torch.int32).cpu().numpy().view(np.uint32)
+        assert np.array_equal(got, want), (n, k, group)
+
+
+def test_dequantize_f32_scale_rounding_unfused(dev):
+    # f32 scales: q*s must round in f32 before + b (no fused multiply-add).
+    n, k = 4, 64
+    codes = np.full((n, k), 15, np.uint8)
+    s = np.full((n, 1), 1.0 + 2.0 ** -23, np.float32)
+    b = np.full((n, 1), 2.0 ** -22, np.float32)
+    out = qkern.dequantize(torch.from_numpy(codes).to(dev),
+                           torch.from_numpy(s).to(dev),
+                           torch.from_numpy(b).to(dev), k=k,
+                           packing=Packing.U8, dtype=torch.float32)
+    torch.cuda.synchronize()
+    want = O.dequantize_f32(codes.reshape(n, 1, k), s[..., None], b[..., None])
+    assert np.array_equal(out.cpu().numpy(), want)
+
+
+# ---------------------------------------------------------------------------
+# BASELINE.json shapes (C4 int8 affine, C5 int4 u32x8) against the C port.
+
+QWEN3_8B = [(4096, 4096), (12288, 4096), (4096, 12288), (151936, 4096)]
+
+
+@pytest.mark.parametrize("nk", QWEN3_8B)
+def test_config_int4_decode(dev, nk):
+    n, k = nk
+    codes, s, b = O.config_affine(n, k, bits=4, seed=0)
+    words = O.pack_u32x8(codes)
+    rng = np.random.default_rng(1)
+    x = O.bf16_round(rng.standard_normal((1, k)).astype(np.float32))
+    y = qkern.qmatvec(torch.from_numpy(x).to(torch.bfloat16).to(dev),
+                      torch.from_numpy(words.view(np.int32)).to(dev),
+                      torch.from_numpy(s).to(torch.bfloat16).to(dev),
+                      torch.from_numpy(b).to(torch.bfloat16).to(dev))
+    torch.cuda.synchronize()
+    want = O.c_matvec_int4_u32x8(O.bf16_bits(x), words, O.bf16_bits(s),
+                                 O.bf16_bits(b))
+    assert O.rel_fro(y.float().cpu().numpy(), want) <= 1e-2
+
+
+@pytest.mark.parametrize("m", [16, 512])
+def test_config_int4_batched(dev, m):
+    n, k = 12288, 4096
+    codes, s, b = O.config_affine(n, k, bits=4, seed=0)
+    words = O.pack_u32x8(codes)
+    rng = np.random.default_rng(2)
+    x = O.bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    y = qkern.qmatvec(torch.from_numpy(x).to(torch.bfloat16).to(dev),
+                      torch.from_numpy(words.view(np.int32)).to(dev),
+                      torch.from_numpy(s).to(torch.bfloat16).to(dev),
+                      torch.from_numpy(b).to(torch.bfloat16).to(dev))
+    torch.cuda.synchronize()
+    rows = sorted(set([0, 1, m // 2, m - 1]))
+    want = O.c_matvec_int4_u32x8(O.bf16_bits(x[rows]), words, O.bf16_bits(s),
+                                 O.bf16_bits(b))
+    assert O.rel_fro(y.float().cpu().numpy()[rows], want) <= 1e-2
+
+
+@pytest.mark.parametrize("m", [1, 8, 128])
+def test_config_int8_affine(dev, m):
+    n, k = 12288, 4096
+    codes, s, b = O.config_affine(n, k, bits=8, seed=0)
+    rng = np.random.default_rng(3)
+    x = O.bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    y = qkern.qmatvec(torch.from_numpy(x).to(torch.bfloat16).to(dev),
+                      torch.from_numpy(codes).to(dev),
+                      torch.from_numpy(s).to(torch.bfloat16).to(dev),
+                      torch.from_numpy(b).to(torch.bfloat16).to(dev),
+                      packing=Packing.U8)
+    torch.cuda.synchronize()
+    rows = sorted(set([0, m // 2, m - 1]))
+    want = O.c_matvec_u8(O.bf16_bits(x[rows]), codes, O.bf16_bits(s),
+                         O.bf16_bits(b))
+    assert O.rel_fro(y.float().cpu().numpy()[rows], want) <= 1e-2
