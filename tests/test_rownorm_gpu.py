@@ -21,11 +21,15 @@ pytestmark = pytest.mark.gpu
 TOL = {"float32": 1e-5, "bfloat16": 8e-3, "float16": 2e-3}
 
 
-def check(got, want, dtype):
+def check(got, want, dtype, beta=None):
     tol = TOL[dtype]
     floor = tol * 1e-3 * np.max(np.abs(want), axis=-1, keepdims=True)
     err = np.abs(got - want)
-    bound = tol * np.abs(want) + floor
+    # with a layer-norm offset the output's error scales with the terms
+    # that are added, not with their (possibly cancelling) sum
+    mag = np.abs(want) if beta is None else \
+        np.abs(want - beta) + np.abs(beta)
+    bound = tol * mag + floor
     assert np.all(err <= bound), float(np.max(err / np.maximum(bound, 1e-30)))
 
 
@@ -44,8 +48,8 @@ def run(dev, kind, x, dtype, gain=None, beta=None, eps=1e-6):
     else:
         want = O.softmax(xr)
     # compare against the oracle rounded once to the output type
-    check(got, O.round_to(want, dtype), dtype) if dtype != "float32" else \
-        check(got, want, dtype)
+    check(got, O.round_to(want, dtype) if dtype != "float32" else want, dtype,
+          beta)
 
 
 SHAPES = [(1, 1), (3, 7), (5, 64), (7, 1000), (2, 129), (4, 4096),
