@@ -91,6 +91,52 @@ qk_status PostLaunch(const char* kernel) {
   return Fail(QK_INTERNAL, "qkern: " + msg);
 }
 
+int DeviceComputeUnits() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount,
+                              dev) != hipSuccess ||
+        cus <= 0) {
+      cus = 256;
+    }
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+int ResidentBlocks(const void* kernel, int block, size_t lds) {
+  struct Key {
+    const void* k;
+    int block;
+    size_t lds;
+    int n;
+  };
+  static std::mutex mu;
+  static Key cache[256];
+  static int used = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < used; ++i) {
+    if (cache[i].k == kernel && cache[i].block == block &&
+        cache[i].lds == lds) {
+      return cache[i].n;
+    }
+  }
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, lds) !=
+          hipSuccess ||
+      n < 1) {
+    (void)hipGetLastError();
+    n = 1;
+  }
+  if (used < 256) cache[used++] = {kernel, block, lds, n};
+  return n;
+}
+
 int DTypeSize(int dtype) {
   switch (dtype) {
     case QK_F32:

@@ -33,6 +33,15 @@ __device__ __forceinline__ bf16 from_f32<bf16>(float v) {
   return static_cast<bf16>(v);
 }
 
+typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Reinterprets 32 bits as two bf16. The argument is a plain value on
+// purpose: clang (ROCm 7.2) miscompiles __builtin_bit_cast applied directly
+// to an element of an ext_vector_type (it reads element 0 for every index).
+__device__ __forceinline__ bf16x2 AsBf16x2(uint32_t u) {
+  return __builtin_bit_cast(bf16x2, u);
+}
+
 // Loads element i of a float buffer whose type is chosen at run time
 // (0 f32, 1 f16, 2 bf16: the qk_dtype values).
 __device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {

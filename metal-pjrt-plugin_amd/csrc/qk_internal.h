@@ -27,6 +27,13 @@ qk_status PreLaunch();
 qk_status PostLaunch(const char* kernel);
 
 int DTypeSize(int dtype);
+
+// Compute units of the current device (cached per device).
+int DeviceComputeUnits();
+
+// Workgroups of `kernel` one CU keeps resident with this block size and
+// dynamic LDS (cached; at least 1).
+int ResidentBlocks(const void* kernel, int block, size_t lds);
 const char* DTypeName(int dtype);
 
 // ---------------------------------------------------------------------------

@@ -23,6 +23,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <string>
 
@@ -33,7 +34,6 @@ namespace qk {
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;  // waves per workgroup
 
@@ -164,9 +164,8 @@ __global__ __launch_bounds__(kWaves * 64) void qmv_int4_bf16_kernel(
         float d = 0.f;
 #pragma unroll
         for (int p = 0; p < 16; ++p)
-          d = __builtin_amdgcn_fdot2_f32_bf16(
-              __builtin_bit_cast(bf16x2, cp[r][p]),
-              __builtin_bit_cast(bf16x2, xp[p]), d, false);
+          d = __builtin_amdgcn_fdot2_f32_bf16(AsBf16x2(cp[r][p]),
+                                              AsBf16x2(xp[p]), d, false);
         acc[mm][r] += s[r] * d + (bb[r] - 128.f * s[r]) * xs;
       }
     }
@@ -343,6 +342,248 @@ __global__ void dequant_kernel(QmvArgs a, long long total_chunks) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Streaming matvec for a few rows of x (M <= 4): the decode hot path.
+//
+// The grid holds about as many waves as the GPU keeps resident; each wave
+// walks output rows gw, gw + GW, ... (GW waves in the grid) and prefetches
+// the next row's codes, scales and offsets into registers while it computes
+// the current row, so every wave keeps one row of loads in flight. Lane l
+// owns the 16-byte chunks l, l + 64, ... of every row, at most CPL of them.
+//
+// x is staged once per workgroup in LDS in the form the chunks consume:
+// for 4-bit codes, bf16 pairs in the order the code words produce them
+// (pair 4i + s of a chunk = nibbles s and s + 4 of word i), for 8-bit
+// codes, f32 values; plus the sum of x over each chunk. The LDS layout is
+// [m][quad][chunk] of 16-byte quads, so the 64 lanes of a wave read
+// consecutive quads (no bank conflicts).
+
+constexpr int kStreamThreads = 256;
+
+template <int PACK>
+struct ChunkTraits {
+  static constexpr bool kInt4 =
+      PACK == QK_PACK_U32X8 || PACK == QK_PACK_BYTE_HALFSPLIT;
+  static constexpr int kCodes = kInt4 ? 32 : 16;  // codes per 16 bytes
+};
+
+// K offset of chunk c's first element and its group (half-split chunks
+// also cover [kb + hg, kb + hg + 16)).
+template <int PACK>
+__device__ __forceinline__ void ChunkSpan(int c, int group, int* kb,
+                                          int* grp) {
+  if (PACK == QK_PACK_BYTE_HALFSPLIT) {
+    const int hg = group / 2;
+    const int byte0 = c * 16;
+    *grp = byte0 / hg;
+    *kb = *grp * group + byte0 % hg;
+  } else {
+    *kb = c * ChunkTraits<PACK>::kCodes;
+    *grp = *kb / group;
+  }
+}
+
+// Element (relative to the chunk's kb) of nibble `nib` of word `i`.
+template <int PACK>
+__device__ __forceinline__ int Int4Elem(int i, int nib, int hg) {
+  if (PACK == QK_PACK_U32X8) return 8 * i + nib;
+  return ((nib & 1) ? hg : 0) + 4 * i + (nib >> 1);
+}
+
+template <int PACK, typename XT>
+__device__ __forceinline__ void StageX(const QmvArgs& a, int mt, int cpr,
+                                       u32x4* xq, float* xs) {
+  const XT* X = static_cast<const XT*>(a.x);
+  const int hg = a.group / 2;
+  for (int idx = threadIdx.x; idx < mt * cpr; idx += kStreamThreads) {
+    const int m = idx / cpr, c = idx % cpr;
+    int kb, grp;
+    ChunkSpan<PACK>(c, a.group, &kb, &grp);
+    const XT* xr = X + static_cast<long long>(m) * a.k + kb;
+    u32x4 quad[4];
+    float sum = 0.f;
+    if constexpr (ChunkTraits<PACK>::kInt4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int sh = 0; sh < 4; ++sh) {
+          const float x0 = to_f32(xr[Int4Elem<PACK>(i, sh, hg)]);
+          const float x1 = to_f32(xr[Int4Elem<PACK>(i, sh + 4, hg)]);
+          sum += x0 + x1;
+          quad[i][sh] = PackBf16Pair(x0, x1);
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float xv = to_f32(xr[4 * i + e]);
+          sum += xv;
+          quad[i][e] = __float_as_uint(xv);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xq[(m * 4 + i) * cpr + c] = quad[i];
+    xs[m * cpr + c] = sum;
+  }
+}
+
+// Partial dot product of one 16-byte chunk of codes with x (m-th row):
+// returns sum_e x_e * q_e, where for 4-bit codes q_e is 128 + code.
+template <int PACK>
+__device__ __forceinline__ float ChunkDot(const u32x4& w, const u32x4* xq,
+                                          int m, int cpr, int c) {
+  float d = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x4 xv = xq[(m * 4 + i) * cpr + c];
+    const uint32_t word = w[i];
+    if constexpr (ChunkTraits<PACK>::kInt4) {
+#pragma unroll
+      for (int sh = 0; sh < 4; ++sh) {
+        const uint32_t cp = ((word >> (4 * sh)) & 0x000F000Fu) | 0x43004300u;
+        const uint32_t xpair = xv[sh];
+        d = __builtin_amdgcn_fdot2_f32_bf16(AsBf16x2(cp), AsBf16x2(xpair), d,
+                                            false);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float q;
+        if (PACK == QK_PACK_S8_SYM)
+          q = static_cast<float>(static_cast<int8_t>(word >> (8 * e)));
+        else
+          q = static_cast<float>((word >> (8 * e)) & 255u);
+        d = fmaf(__uint_as_float(xv[e]), q, d);
+      }
+    }
+  }
+  return d;
+}
+
+template <int PACK, typename XT, int MT, int CPL>
+__global__ __launch_bounds__(kStreamThreads) void qmv_stream_kernel(
+    QmvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int cpr = a.row_bytes / 16;
+  u32x4* xq = reinterpret_cast<u32x4*>(smem);
+  float* xs = reinterpret_cast<float*>(smem + MT * 4 * cpr * 16);
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * (kStreamThreads / 64) + (threadIdx.x >> 6);
+  const int GW = gridDim.x * (kStreamThreads / 64);
+  const int groups = a.k / a.group;
+  constexpr bool kInt4 = ChunkTraits<PACK>::kInt4;
+
+  // Codes, scales and offsets of one row for this lane's chunks.
+  struct RowRegs {
+    u32x4 w[CPL];
+    float s[CPL], b[CPL];
+  };
+  auto load_row = [&](int row, RowRegs& r) {
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + 64 * j;
+      if (c < cpr) {
+        r.w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+            a.codes + static_cast<long long>(row) * a.row_bytes + c * 16));
+        int kb, grp;
+        ChunkSpan<PACK>(c, a.group, &kb, &grp);
+        const long long gi = static_cast<long long>(row) * groups + grp;
+        r.s[j] = load_any(a.scales, gi, a.sdt);
+        r.b[j] = a.has_bias ? load_any(a.biases, gi, a.bdt) : 0.f;
+      }
+    }
+  };
+
+  RowRegs cur, nxt;
+  int row = gw;
+  if (row < a.n) load_row(row, cur);  // in flight while x is staged
+  StageX<PACK, XT>(a, a.m, cpr, xq, xs);
+  __syncthreads();
+
+  for (; row < a.n; row += GW) {
+    const int nrow = row + GW;
+    if (nrow < a.n) load_row(nrow, nxt);
+    float acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + 64 * j;
+      if (c >= cpr) continue;
+      // 4-bit codes carry +128 (see ChunkDot): fold it into the offset.
+      const float boff = kInt4 ? cur.b[j] - 128.f * cur.s[j] : cur.b[j];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        if (m >= a.m) break;
+        const float d = ChunkDot<PACK>(cur.w[j], xq, m, cpr, c);
+        acc[m] = fmaf(cur.s[j], d, fmaf(boff, xs[m * cpr + c], acc[m]));
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m >= a.m) break;
+      const float v = wave_sum(acc[m]);
+      if (lane == 0)
+        static_cast<XT*>(a.y)[static_cast<long long>(m) * a.n + row] =
+            from_f32<XT>(v);
+    }
+    cur = nxt;
+  }
+}
+
+template <int PACK, typename XT, int MT>
+qk_status LaunchStreamMT(QmvArgs a, int cpl, int cus, hipStream_t st) {
+  const int cpr = a.row_bytes / 16;
+  const size_t lds = static_cast<size_t>(MT) * cpr * (64 + 4);
+  const int rows_per_wg = kStreamThreads / 64;
+  const int need = (a.n + rows_per_wg - 1) / rows_per_wg;
+  // As many workgroups as the GPU keeps resident (each wave then walks
+  // its rows with a prefetch), at most one row per wave.
+  auto go = [&](auto kernel) {
+    const int per_cu = ResidentBlocks(reinterpret_cast<const void*>(kernel),
+                                      kStreamThreads, lds);
+    const int grid = std::max(1, std::min(need, cus * per_cu));
+    kernel<<<grid, kStreamThreads, lds, st>>>(a);
+    return PostLaunch("qmv_stream");
+  };
+  switch (cpl) {
+    case 1:
+      return go(qmv_stream_kernel<PACK, XT, MT, 1>);
+    case 2:
+      return go(qmv_stream_kernel<PACK, XT, MT, 2>);
+    case 3:
+      return go(qmv_stream_kernel<PACK, XT, MT, 3>);
+    case 4:
+      return go(qmv_stream_kernel<PACK, XT, MT, 4>);
+    case 6:
+      return go(qmv_stream_kernel<PACK, XT, MT, 6>);
+    default:
+      return go(qmv_stream_kernel<PACK, XT, MT, 8>);
+  }
+}
+
+// M <= 4 rows; false when this path does not apply (then *st is unset).
+template <int PACK, typename XT>
+bool LaunchStream(const QmvArgs& a, int cus, hipStream_t stream,
+                  qk_status* st) {
+  const int cpr = a.row_bytes / 16;
+  int cpl = (cpr + 63) / 64;
+  if (cpl > 8 || a.m > 4) return false;
+  if (cpl == 5) cpl = 6;
+  if (cpl == 7) cpl = 8;
+  const int mt = a.m <= 1 ? 1 : a.m <= 2 ? 2 : 4;
+  const size_t lds = static_cast<size_t>(mt) * cpr * (64 + 4);
+  if (lds > 64 * 1024) return false;
+  if (mt == 1)
+    *st = LaunchStreamMT<PACK, XT, 1>(a, cpl, cus, stream);
+  else if (mt == 2)
+    *st = LaunchStreamMT<PACK, XT, 2>(a, cpl, cus, stream);
+  else
+    *st = LaunchStreamMT<PACK, XT, 4>(a, cpl, cus, stream);
+  return true;
+}
+
 int RowBytes(const QuantProblem& p) {
   return static_cast<int>(p.bits == 4 ? p.k / 2 : p.k);
 }
@@ -432,6 +673,28 @@ qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream) {
   }
   QmvArgs a = MakeArgs(p);
   const int m = static_cast<int>(p.m);
+  if (m <= 4) {
+    const int cus = DeviceComputeUnits();
+    qk_status st = QK_OK;
+    bool done = false;
+    if (p.x_dtype == QK_BF16 && p.packing == QK_PACK_U32X8)
+      done = LaunchStream<QK_PACK_U32X8, bf16>(a, cus, stream, &st);
+    else if (p.x_dtype == QK_BF16 && p.packing == QK_PACK_BYTE_HALFSPLIT)
+      done = LaunchStream<QK_PACK_BYTE_HALFSPLIT, bf16>(a, cus, stream, &st);
+    else if (p.packing == QK_PACK_U8 || p.packing == QK_PACK_S8_SYM) {
+      const bool u8 = p.packing == QK_PACK_U8;
+      if (p.x_dtype == QK_BF16)
+        done = u8 ? LaunchStream<QK_PACK_U8, bf16>(a, cus, stream, &st)
+                  : LaunchStream<QK_PACK_S8_SYM, bf16>(a, cus, stream, &st);
+      else if (p.x_dtype == QK_F16)
+        done = u8 ? LaunchStream<QK_PACK_U8, f16>(a, cus, stream, &st)
+                  : LaunchStream<QK_PACK_S8_SYM, f16>(a, cus, stream, &st);
+      else
+        done = u8 ? LaunchStream<QK_PACK_U8, float>(a, cus, stream, &st)
+                  : LaunchStream<QK_PACK_S8_SYM, float>(a, cus, stream, &st);
+    }
+    if (done) return st;
+  }
   if (p.x_dtype == QK_BF16 && p.packing == QK_PACK_U32X8)
     return LaunchInt4Bf16<QK_PACK_U32X8>(a, m, stream);
   if (p.x_dtype == QK_BF16 && p.packing == QK_PACK_BYTE_HALFSPLIT)

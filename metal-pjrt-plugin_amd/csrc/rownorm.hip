@@ -8,12 +8,15 @@
 //   RMS:     y = x * rsqrt(sum(x^2)/n + eps) * gain
 //   LAYER:   mu = sum(x)/n, var = sum((x-mu)^2)/n,
 //            y = (x - mu) / sqrt(var + eps) * gain + beta
-//   SOFTMAX: y = exp(x - max) / sum(exp(x - max))
+//   SOFTMAX: y = exp(x - max) * (1 / sum(exp(x - max)))
 //
-// Each row is read once into registers with 16-byte loads (a workgroup of
-// 256 threads per long row, one wavefront per short row), reduced with
-// wavefront butterflies plus one LDS exchange, and written once. Rows too
-// long for registers take a looping kernel that reads them again.
+// Each row is read once into registers with 16-byte loads, reduced with
+// wavefront butterflies (plus one LDS exchange when four waves share a
+// row), and written once with 16-byte stores. Rows up to 16 vectors per
+// lane of one wavefront take one wavefront each (no barriers); longer rows
+// take a 256-thread workgroup; rows too long for registers take a looping
+// kernel that reads them again. The kind is a template parameter; gain and
+// beta types are chosen per 16-byte vector (a uniform branch).
 
 #include <hip/hip_runtime.h>
 
@@ -34,7 +37,6 @@ struct RnArgs {
   const void* beta;
   long long rows;
   int n;
-  int kind;
   float eps;
   int gdt, bdt;
   int has_gain, has_beta;
@@ -53,10 +55,7 @@ __device__ __forceinline__ float row_sum(float v, float* red) {
     __syncthreads();  // red may still be read by a previous reduction
     if ((threadIdx.x & 63) == 0) red[wave] = v;
     __syncthreads();
-    float s = 0.f;
-#pragma unroll
-    for (int w = 0; w < TPR / 64; ++w) s += red[w];
-    return s;
+    return (red[0] + red[1]) + (red[2] + red[3]);
   }
 }
 template <int TPR>
@@ -69,53 +68,92 @@ __device__ __forceinline__ float row_max(float v, float* red) {
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[wave] = v;
     __syncthreads();
-    float s = red[0];
-#pragma unroll
-    for (int w = 1; w < TPR / 64; ++w) s = fmaxf(s, red[w]);
-    return s;
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   }
 }
 
-// V elements per load (16 bytes, or 1 when rows are not 16-byte aligned),
-// VPT loads per thread, TPR threads per row.
-template <typename T, int V, int VPT, int TPR>
+// V consecutive elements starting at element i of a float vector of type
+// dtype (qk_dtype), as f32. vec: 16-byte aligned loads are allowed.
+template <int V>
+__device__ __forceinline__ void load_param(const void* p, int dtype, int i,
+                                           bool vec, float* out) {
+  if (vec && V > 1) {
+    if (dtype == QK_F32) {
+#pragma unroll
+      for (int h = 0; h < V / 4; ++h) {
+        const u32x4 q = *reinterpret_cast<const u32x4*>(
+            static_cast<const float*>(p) + i + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[4 * h + e] = __uint_as_float(q[e]);
+      }
+      return;
+    }
+    if (V % 8 == 0) {
+#pragma unroll
+      for (int h = 0; h < V / 8; ++h) {
+        const u32x4 q = *reinterpret_cast<const u32x4*>(
+            static_cast<const uint16_t*>(p) + i + 8 * h);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t bits = (q[e / 2] >> (16 * (e & 1))) & 0xffffu;
+          out[8 * h + e] =
+              dtype == QK_BF16
+                  ? __uint_as_float(bits << 16)
+                  : static_cast<float>(__builtin_bit_cast(f16,
+                                                          static_cast<uint16_t>(bits)));
+        }
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < V; ++e) out[e] = load_any(p, i + e, dtype);
+}
+
+// V elements per access (16 bytes, or 1 when rows are not 16-byte
+// aligned), VPT accesses per thread, TPR threads per row.
+template <typename T, int KIND, int V, int VPT, int TPR>
 __global__ __launch_bounds__(kThreads) void rownorm_kernel(RnArgs a) {
   __shared__ float red[kThreads / 64];
   constexpr int RPB = kThreads / TPR;  // rows per block
   const int t = threadIdx.x % TPR;
   const long long row = static_cast<long long>(blockIdx.x) * RPB +
                         threadIdx.x / TPR;
-  // TPR == 256: the whole block shares the row, so this exit is uniform.
+  // TPR == 256: the whole block shares the row, so this exit is uniform;
+  // TPR == 64: whole wavefronts exit, and no barrier follows.
   if (row >= a.rows) return;
   const T* xr = static_cast<const T*>(a.x) + row * a.n;
   T* yr = static_cast<T*>(a.y) + row * a.n;
   const int n = a.n;
 
+  union Pack {
+    u32x4 u;
+    T e[V > 1 ? V : 1];
+  };
   float v[VPT][V];
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int base = (t + i * TPR) * V;
-    if constexpr (V > 1) {
-      if (base < n) {
-        union {
-          u32x4 u;
-          T e[V];
-        } q;
-        q.u = *reinterpret_cast<const u32x4*>(xr + base);
+    if (base < n) {
+      if constexpr (V > 1) {
+        Pack q;
+        q.u = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(xr + base));
 #pragma unroll
         for (int e = 0; e < V; ++e) v[i][e] = to_f32(q.e[e]);
       } else {
-#pragma unroll
-        for (int e = 0; e < V; ++e) v[i][e] = 0.f;
+        v[i][0] = to_f32(xr[base]);
       }
     } else {
-      v[i][0] = base < n ? to_f32(xr[base]) : 0.f;
+#pragma unroll
+      for (int e = 0; e < V; ++e) v[i][e] = KIND == QK_ROWNORM_SOFTMAX
+                                                ? -INFINITY
+                                                : 0.f;
     }
   }
-  auto valid = [&](int i) { return (t + i * TPR) * V < n; };
 
   float scale = 1.f, shift = 0.f;  // y = (x - shift) * scale (then gain)
-  if (a.kind == QK_ROWNORM_RMS) {
+  if constexpr (KIND == QK_ROWNORM_RMS) {
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
@@ -123,7 +161,7 @@ __global__ __launch_bounds__(kThreads) void rownorm_kernel(RnArgs a) {
       for (int e = 0; e < V; ++e) ss += v[i][e] * v[i][e];
     ss = row_sum<TPR>(ss, red);
     scale = rsqrtf(ss / static_cast<float>(n) + a.eps);
-  } else if (a.kind == QK_ROWNORM_LAYER) {
+  } else if constexpr (KIND == QK_ROWNORM_LAYER) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
@@ -132,13 +170,14 @@ __global__ __launch_bounds__(kThreads) void rownorm_kernel(RnArgs a) {
     const float mu = row_sum<TPR>(s, red) / static_cast<float>(n);
     float q = 0.f;
 #pragma unroll
-    for (int i = 0; i < VPT; ++i)
-      if (valid(i))
+    for (int i = 0; i < VPT; ++i) {
+      if ((t + i * TPR) * V >= n) continue;
 #pragma unroll
-        for (int e = 0; e < V; ++e) {
-          const float d = v[i][e] - mu;
-          q += d * d;
-        }
+      for (int e = 0; e < V; ++e) {
+        const float d = v[i][e] - mu;
+        q += d * d;
+      }
+    }
     const float var = row_sum<TPR>(q, red) / static_cast<float>(n);
     shift = mu;
     scale = 1.0f / sqrtf(var + a.eps);
@@ -146,49 +185,49 @@ __global__ __launch_bounds__(kThreads) void rownorm_kernel(RnArgs a) {
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
-      if (valid(i))
 #pragma unroll
-        for (int e = 0; e < V; ++e) mx = fmaxf(mx, v[i][e]);
+      for (int e = 0; e < V; ++e) mx = fmaxf(mx, v[i][e]);
     mx = row_max<TPR>(mx, red);
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
-      if (valid(i))
 #pragma unroll
-        for (int e = 0; e < V; ++e) {
-          v[i][e] = expf(v[i][e] - mx);
-          s += v[i][e];
-        }
+      for (int e = 0; e < V; ++e) {
+        v[i][e] = __expf(v[i][e] - mx);
+        s += v[i][e];
+      }
     s = row_sum<TPR>(s, red);
-    shift = 0.f;
-    scale = s;  // divided below
+    scale = 1.0f / s;
   }
 
+  const bool gvec = V > 1 && (reinterpret_cast<uintptr_t>(a.gain) % 16 == 0);
+  const bool bvec = V > 1 && (reinterpret_cast<uintptr_t>(a.beta) % 16 == 0);
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    if (!valid(i)) continue;
     const int base = (t + i * TPR) * V;
+    if (base >= n) continue;
     float out[V];
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
-      float o;
-      if (a.kind == QK_ROWNORM_SOFTMAX) {
-        o = v[i][e] / scale;
-      } else {
-        o = (v[i][e] - shift) * scale;
-        if (a.has_gain) o *= load_any(a.gain, base + e, a.gdt);
-        if (a.has_beta) o += load_any(a.beta, base + e, a.bdt);
+    for (int e = 0; e < V; ++e) out[e] = (v[i][e] - shift) * scale;
+    if constexpr (KIND != QK_ROWNORM_SOFTMAX) {
+      if (a.has_gain) {
+        float g[V];
+        load_param<V>(a.gain, a.gdt, base, gvec, g);
+#pragma unroll
+        for (int e = 0; e < V; ++e) out[e] *= g[e];
       }
-      out[e] = o;
+      if (KIND == QK_ROWNORM_LAYER && a.has_beta) {
+        float bb[V];
+        load_param<V>(a.beta, a.bdt, base, bvec, bb);
+#pragma unroll
+        for (int e = 0; e < V; ++e) out[e] += bb[e];
+      }
     }
     if constexpr (V > 1) {
-      union {
-        u32x4 u;
-        T e[V];
-      } q;
+      Pack q;
 #pragma unroll
       for (int e = 0; e < V; ++e) q.e[e] = from_f32<T>(out[e]);
-      *reinterpret_cast<u32x4*>(yr + base) = q.u;
+      __builtin_nontemporal_store(q.u, reinterpret_cast<u32x4*>(yr + base));
     } else {
       yr[base] = from_f32<T>(out[0]);
     }
@@ -197,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void rownorm_kernel(RnArgs a) {
 
 // Rows longer than the register kernels take: one block per row, reading
 // the row once per statistic.
-template <typename T>
+template <typename T, int KIND>
 __global__ __launch_bounds__(kThreads) void rownorm_long_kernel(RnArgs a) {
   __shared__ float red[kThreads / 64];
   const long long row = blockIdx.x;
@@ -205,7 +244,7 @@ __global__ __launch_bounds__(kThreads) void rownorm_long_kernel(RnArgs a) {
   T* yr = static_cast<T*>(a.y) + row * a.n;
   const int n = a.n;
   float scale = 1.f, shift = 0.f;
-  if (a.kind == QK_ROWNORM_RMS) {
+  if constexpr (KIND == QK_ROWNORM_RMS) {
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += kThreads) {
       const float x = to_f32(xr[i]);
@@ -213,7 +252,7 @@ __global__ __launch_bounds__(kThreads) void rownorm_long_kernel(RnArgs a) {
     }
     ss = row_sum<kThreads>(ss, red);
     scale = rsqrtf(ss / static_cast<float>(n) + a.eps);
-  } else if (a.kind == QK_ROWNORM_LAYER) {
+  } else if constexpr (KIND == QK_ROWNORM_LAYER) {
     float s = 0.f;
     for (int i = threadIdx.x; i < n; i += kThreads) s += to_f32(xr[i]);
     const float mu = row_sum<kThreads>(s, red) / static_cast<float>(n);
@@ -232,10 +271,11 @@ __global__ __launch_bounds__(kThreads) void rownorm_long_kernel(RnArgs a) {
     mx = row_max<kThreads>(mx, red);
     float s = 0.f;
     for (int i = threadIdx.x; i < n; i += kThreads)
-      s += expf(to_f32(xr[i]) - mx);
+      s += __expf(to_f32(xr[i]) - mx);
     s = row_sum<kThreads>(s, red);
+    const float inv = 1.0f / s;
     for (int i = threadIdx.x; i < n; i += kThreads)
-      yr[i] = from_f32<T>(expf(to_f32(xr[i]) - mx) / s);
+      yr[i] = from_f32<T>(__expf(to_f32(xr[i]) - mx) * inv);
     return;
   }
   for (int i = threadIdx.x; i < n; i += kThreads) {
@@ -246,43 +286,40 @@ __global__ __launch_bounds__(kThreads) void rownorm_long_kernel(RnArgs a) {
   }
 }
 
-template <typename T, int V, int TPR>
-qk_status LaunchVpt(const RnArgs& a, hipStream_t st) {
-  const int per = TPR * V;  // elements per VPT step
-  const long long rpb = kThreads / TPR;
-  dim3 grid(static_cast<unsigned>((a.rows + rpb - 1) / rpb)), block(kThreads);
-  if (a.n <= per)
-    rownorm_kernel<T, V, 1, TPR><<<grid, block, 0, st>>>(a);
-  else if (a.n <= 2 * per)
-    rownorm_kernel<T, V, 2, TPR><<<grid, block, 0, st>>>(a);
-  else if (a.n <= 4 * per)
-    rownorm_kernel<T, V, 4, TPR><<<grid, block, 0, st>>>(a);
-  else if (a.n <= 8 * per)
-    rownorm_kernel<T, V, 8, TPR><<<grid, block, 0, st>>>(a);
-  else
-    rownorm_kernel<T, V, 16, TPR><<<grid, block, 0, st>>>(a);
+template <typename T, int KIND, int V>
+qk_status LaunchV(const RnArgs& a, hipStream_t st) {
+  constexpr int kSmall = 64 * V * 4, kWave = 64 * V * 16,
+                kBlock = kThreads * V * 16;
+  if (a.n <= kSmall) {
+    dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
+    rownorm_kernel<T, KIND, V, 4, 64><<<grid, kThreads, 0, st>>>(a);
+  } else if (a.n <= kWave) {
+    dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
+    rownorm_kernel<T, KIND, V, 16, 64><<<grid, kThreads, 0, st>>>(a);
+  } else if (a.n <= kBlock) {
+    dim3 grid(static_cast<unsigned>(a.rows));
+    rownorm_kernel<T, KIND, V, 16, kThreads><<<grid, kThreads, 0, st>>>(a);
+  } else {
+    dim3 grid(static_cast<unsigned>(a.rows));
+    rownorm_long_kernel<T, KIND><<<grid, kThreads, 0, st>>>(a);
+  }
   return PostLaunch("rownorm");
 }
 
-template <typename T>
-qk_status LaunchTyped(const RnArgs& a, hipStream_t st) {
+template <typename T, int KIND>
+qk_status LaunchKind(const RnArgs& a, hipStream_t st) {
   constexpr int V = 16 / sizeof(T);
   const bool aligned = (reinterpret_cast<uintptr_t>(a.x) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) &&
                        (static_cast<long long>(a.n) * sizeof(T)) % 16 == 0;
-  if (aligned) {
-    if (a.n <= 64 * V * 4) return LaunchVpt<T, V, 64>(a, st);
-    if (a.n <= kThreads * V * 16) return LaunchVpt<T, V, kThreads>(a, st);
-  } else {
-    if (a.n <= 64 * 4) return LaunchVpt<T, 1, 64>(a, st);
-    if (a.n <= kThreads * 16) return LaunchVpt<T, 1, kThreads>(a, st);
-  }
-  if (a.rows > 0x7fffffff) {
-    return Fail(QK_UNIMPLEMENTED, "qkern: rownorm has too many rows");
-  }
-  rownorm_long_kernel<T><<<dim3(static_cast<unsigned>(a.rows)), kThreads, 0,
-                           st>>>(a);
-  return PostLaunch("rownorm_long");
+  return aligned ? LaunchV<T, KIND, V>(a, st) : LaunchV<T, KIND, 1>(a, st);
+}
+
+template <typename T>
+qk_status LaunchTyped(const RnArgs& a, int kind, hipStream_t st) {
+  if (kind == QK_ROWNORM_RMS) return LaunchKind<T, QK_ROWNORM_RMS>(a, st);
+  if (kind == QK_ROWNORM_LAYER) return LaunchKind<T, QK_ROWNORM_LAYER>(a, st);
+  return LaunchKind<T, QK_ROWNORM_SOFTMAX>(a, st);
 }
 
 }  // namespace
@@ -301,7 +338,6 @@ qk_status LaunchRownorm(const RownormProblem& p, hipStream_t stream) {
   a.beta = p.beta;
   a.rows = p.rows;
   a.n = static_cast<int>(p.n);
-  a.kind = p.kind;
   a.eps = p.eps;
   a.gdt = p.gain_dtype;
   a.bdt = p.beta_dtype;
@@ -309,11 +345,11 @@ qk_status LaunchRownorm(const RownormProblem& p, hipStream_t stream) {
   a.has_beta = p.beta != nullptr;
   switch (p.dtype) {
     case QK_BF16:
-      return LaunchTyped<bf16>(a, stream);
+      return LaunchTyped<bf16>(a, p.kind, stream);
     case QK_F16:
-      return LaunchTyped<f16>(a, stream);
+      return LaunchTyped<f16>(a, p.kind, stream);
     default:
-      return LaunchTyped<float>(a, stream);
+      return LaunchTyped<float>(a, p.kind, stream);
   }
 }
 
