@@ -25,6 +25,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 #include <string>
 
 #include "qk_device.h"
@@ -54,6 +55,7 @@ struct GemmArgs {
   int use_c, has_bias, has_aux, act;
   int out_f32;    // D (and C, bias, aux) are f32; else the input type
   int a_vec, b_vec;  // operand allows 16-byte vector loads
+  int out_vec;       // D rows allow 4-element vector stores
   int tiles_m, tiles_n;
 };
 
@@ -340,6 +342,283 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_mfma_kernel(GemmArgs g) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// f16/bf16 kernel: every operand tile is copied into LDS in its source
+// orientation with 16-byte stores (no transposition on the way in), and
+// MFMA fragments are read with ds_read_b128 when the operand is
+// K-contiguous, or with the gfx950 transposing read ds_read_b64_tr_b16
+// when it is M/N-contiguous (B in the NN layout, A when transposed).
+//
+// ds_read_b64_tr_b16, per group of 16 lanes: lane s supplies the address of
+// 4 consecutive 16-bit elements; lane L receives element L%4 of the chunks
+// of lanes L/4, 4 + L/4, 8 + L/4, 12 + L/4. With lane s pointing at
+// X[k0 + s/4][r0 + 4*(s%4)] of a K-major tile X[k][r], lane L receives
+// X[k0..k0+3][r0 + L]: four consecutive K elements of row r0 + L, the
+// MFMA operand layout. Two such reads give the 8 K elements of a
+// v_mfma_f32_32x32x16 operand.
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+template <typename T>
+__device__ __forceinline__ u32x2 lds_read_tr(const T* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s16x4*)(const_cast<T*>(p)));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// LDS tile of R rows (M or N) x BK: K-contiguous [R][BK + 8] when KCONT,
+// else K-major [BK][R + 16] (the source orientation in both cases).
+template <typename T, int R, int BK, bool KCONT>
+struct TileLayout {
+  static constexpr int kLd = KCONT ? BK + 8 : R + 16;
+  static constexpr int kElems = KCONT ? R * kLd : BK * kLd;
+};
+
+// Global -> registers -> LDS copy of one tile in its source orientation.
+template <typename T, int R, int BK, int NT, bool KCONT>
+struct DirectLoader {
+  static constexpr int VPR = (KCONT ? BK : R) / 8;  // vectors per source row
+  static constexpr int NV = R * BK / 8 / NT;        // vectors per thread
+  static_assert(NV * NT * 8 == R * BK, "tile does not split evenly");
+  u32x4 v[NV];
+
+  // src: operand batch base; the tile covers rows [r0, r0+R) and K
+  // [k0, k0+BK); ld is the source row stride (elements).
+  __device__ __forceinline__ void load(const T* __restrict__ src, int ld,
+                                       int r0, int k0, int rows_total,
+                                       int k_total, bool vec_ok, int tid) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int id = tid + i * NT;
+      const int sr = id / VPR, sc = (id % VPR) * 8;  // source row / column
+      // K-contiguous: source row = tile row, column = k; else row = k.
+      const int gr = KCONT ? r0 + sr : k0 + sr;
+      const int gc = KCONT ? k0 + sc : r0 + sc;
+      const int rlim = KCONT ? rows_total : k_total;
+      const int clim = KCONT ? k_total : rows_total;
+      const T* p = src + static_cast<long long>(gr) * ld + gc;
+      if (vec_ok && gr < rlim && gc + 8 <= clim) {
+        v[i] = *reinterpret_cast<const u32x4*>(p);
+      } else {
+        union {
+          u32x4 u;
+          T e[8];
+        } t;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          t.e[e] = (gr < rlim && gc + e < clim) ? p[e] : T(0);
+        v[i] = t.u;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(T* lds, int tid) const {
+    constexpr int LD = TileLayout<T, R, BK, KCONT>::kLd;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int id = tid + i * NT;
+      const int sr = id / VPR, sc = (id % VPR) * 8;
+      *reinterpret_cast<u32x4*>(lds + sr * LD + sc) = v[i];
+    }
+  }
+};
+
+// MFMA operand fragment for rows [rb, rb + 32) and K [kb, kb + 16) of an
+// LDS tile (see TileLayout); lane l gets row rb + l%32, K kb + 8*(l/32)..+8.
+template <typename T, int R, int BK, bool KCONT>
+__device__ __forceinline__ typename Frag<T>::type load_frag(const T* lds,
+                                                            int rb, int kb,
+                                                            int lane) {
+  constexpr int LD = TileLayout<T, R, BK, KCONT>::kLd;
+  if constexpr (KCONT) {
+    return *reinterpret_cast<const typename Frag<T>::type*>(
+        lds + (rb + (lane & 31)) * LD + kb + (lane >> 5) * 8);
+  } else {
+    const int g = lane >> 4, s = lane & 15;
+    const T* p = lds + (kb + 8 * (g >> 1) + (s >> 2)) * LD + rb +
+                 16 * (g & 1) + 4 * (s & 3);
+    const u32x2 lo = lds_read_tr(p);
+    const u32x2 hi = lds_read_tr(p + 4 * LD);
+    const u32x4 q = {lo[0], lo[1], hi[0], hi[1]};
+    return __builtin_bit_cast(typename Frag<T>::type, q);
+  }
+}
+
+template <typename T, int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs g) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr bool AK = !TA, BKC = TB;  // K-contiguous operands
+  using LA = TileLayout<T, BM, BK, AK>;
+  using LB = TileLayout<T, BN, BK, BKC>;
+  static_assert(FM >= 1 && FN >= 1 && BK % 16 == 0, "bad tile");
+
+  // One LDS block: two stages of the A and B tiles during the K loop, the
+  // f32 output tile (in row slabs) in the epilogue.
+  constexpr int kTileBytes = 2 * (LA::kElems + LB::kElems) * sizeof(T);
+  constexpr int kLdo = BN + 4;  // f32 staging row stride
+  constexpr int kSlab = WTM;    // output rows staged at a time
+  constexpr int kOutBytes = kSlab * kLdo * 4;
+  __shared__ __attribute__((aligned(16)))
+  unsigned char lds_raw[kTileBytes > kOutBytes ? kTileBytes : kOutBytes];
+  T* const lds_base = reinterpret_cast<T*>(lds_raw);
+  auto lds_a = [&](int stage) { return lds_base + stage * LA::kElems; };
+  auto lds_b = [&](int stage) {
+    return lds_base + 2 * LA::kElems + stage * LB::kElems;
+  };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int nwg = g.tiles_m * g.tiles_n;
+  int bid = blockIdx.x;
+  if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+  const int group_span = kGroupM * g.tiles_n;
+  const int first_m = (bid / group_span) * kGroupM;
+  const int gsz = min(g.tiles_m - first_m, kGroupM);
+  const int tm = first_m + (bid % group_span) % gsz;
+  const int tn = (bid % group_span) / gsz;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const long long batch = blockIdx.y;
+
+  const T* A = static_cast<const T*>(g.a) + batch * g.bsa;
+  const T* B = static_cast<const T*>(g.b) + batch * g.bsb;
+
+  DirectLoader<T, BM, BK, NT, AK> la;
+  DirectLoader<T, BN, BK, NT, BKC> lb;
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int ktiles = (g.k + BK - 1) / BK;
+  if (ktiles > 0) {
+    la.load(A, g.lda, m0, 0, g.m, g.k, g.a_vec, tid);
+    lb.load(B, g.ldb, n0, 0, g.n, g.k, g.b_vec, tid);
+    la.store(lds_a(0), tid);
+    lb.store(lds_b(0), tid);
+    __syncthreads();
+  }
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < ktiles;
+    if (more) {
+      la.load(A, g.lda, m0, (kt + 1) * BK, g.m, g.k, g.a_vec, tid);
+      lb.load(B, g.ldb, n0, (kt + 1) * BK, g.n, g.k, g.b_vec, tid);
+    }
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      typename Frag<T>::type fa[FM], fb[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        fa[i] = load_frag<T, BM, BK, AK>(lds_a(cur), wm * WTM + i * 32,
+                                         ks * 16, lane);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        fb[j] = load_frag<T, BN, BK, BKC>(lds_b(cur), wn * WTN + j * 32,
+                                          ks * 16, lane);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) mma(acc[i][j], fa[i], fb[j]);
+    }
+    if (more) {
+      la.store(lds_a(cur ^ 1), tid);
+      lb.store(lds_b(cur ^ 1), tid);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue through LDS, one slab of WTM output rows (one row of waves)
+  // at a time: the waves of that row write their f32 accumulators, then
+  // all threads apply alpha, beta*C, bias, aux and the activation to four
+  // consecutive columns each and store them with one vector store.
+  const bool of32 = g.out_f32 != 0;
+  const long long dbase = batch * g.bsd;
+  float* stage = reinterpret_cast<float*>(lds_raw);
+  const bool vec_out = g.out_vec != 0;
+#pragma unroll 1
+  for (int slab = 0; slab < WM; ++slab) {
+    if (wm == slab) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int col = wn * WTN + j * 32 + (lane & 31);
+            stage[row * kLdo + col] = acc[i][j][r];
+          }
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int q = tid; q < kSlab * BN / 4; q += NT) {
+      const int lr = q / (BN / 4), lc = (q % (BN / 4)) * 4;
+      const int row = m0 + slab * WTM + lr, col = n0 + lc;
+      if (row >= g.m || col >= g.n) continue;
+      const float4 a4 = *reinterpret_cast<const float4*>(stage + lr * kLdo + lc);
+      float v[4] = {a4.x, a4.y, a4.z, a4.w};
+      const long long idx = dbase + static_cast<long long>(row) * g.ldd + col;
+      const int cnt = min(4, g.n - col);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (e >= cnt) break;
+        float x = g.alpha * v[e];
+        if (g.use_c) x += g.beta * ld_out<T>(g.c, idx + e, of32);
+        if (g.has_bias) x += ld_out<T>(g.bias, col + e, of32);
+        if (g.has_aux) st_out<T>(g.aux, idx + e, of32, x);
+        v[e] = act_f32(g.act, x);
+      }
+      if (vec_out && cnt == 4) {
+        if (of32) {
+          *reinterpret_cast<float4*>(static_cast<float*>(g.d) + idx) =
+              make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+          union {
+            u32x2 u;
+            T e[4];
+          } o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o.e[e] = from_f32<T>(v[e]);
+          *reinterpret_cast<u32x2*>(static_cast<T*>(g.d) + idx) = o.u;
+        }
+      } else {
+        for (int e = 0; e < cnt; ++e) st_out<T>(g.d, idx + e, of32, v[e]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <typename T, int BM, int BN, int BK, int WM, int WN>
+qk_status DispatchTile(const GemmArgs& g, int batch, bool ta, bool tb,
+                       hipStream_t stream, const char* name) {
+  dim3 grid(g.tiles_m * g.tiles_n, batch);
+  dim3 block(WM * WN * 64);
+  if (!ta && !tb)
+    gemm_tile_kernel<T, BM, BN, BK, WM, WN, false, false>
+        <<<grid, block, 0, stream>>>(g);
+  else if (!ta && tb)
+    gemm_tile_kernel<T, BM, BN, BK, WM, WN, false, true>
+        <<<grid, block, 0, stream>>>(g);
+  else if (ta && !tb)
+    gemm_tile_kernel<T, BM, BN, BK, WM, WN, true, false>
+        <<<grid, block, 0, stream>>>(g);
+  else
+    gemm_tile_kernel<T, BM, BN, BK, WM, WN, true, true>
+        <<<grid, block, 0, stream>>>(g);
+  return PostLaunch(name);
+}
+
 struct TileCfg {
   int bm, bn, bk, wm, wn;
 };
@@ -368,6 +647,31 @@ int64_t CeilDiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace
 
+// f16/bf16 tile configurations: BM, BN, waves along M, waves along N.
+struct HalfTile {
+  int bm, bn, wm, wn;
+};
+constexpr HalfTile kHalfTiles[] = {
+    {256, 256, 2, 2},  // 0: 128x128 per wave, one wave per SIMD
+    {256, 256, 2, 4},  // 1: 128x64 per wave
+    {128, 128, 2, 2},  // 2
+    {64, 64, 2, 2},    // 3
+    {256, 128, 2, 2},  // 4
+    {128, 256, 2, 2},  // 5
+};
+constexpr int kNumHalfTiles = sizeof(kHalfTiles) / sizeof(kHalfTiles[0]);
+
+// QK_GEMM_TILE=<index into kHalfTiles> forces a configuration (tuning).
+int ForcedHalfTile() {
+  static const int forced = [] {
+    const char* v = std::getenv("QK_GEMM_TILE");
+    if (v == nullptr || *v < '0' || *v > '9') return -1;
+    const int t = std::atoi(v);
+    return t >= 0 && t < kNumHalfTiles ? t : -1;
+  }();
+  return forced;
+}
+
 GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
   GemmKernelChoice c;
   const bool half = p.a.dtype != QK_F32;
@@ -376,13 +680,22 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
     return CeilDiv(p.m, bm) * CeilDiv(p.n, bn) * batch;
   };
   if (half) {
-    if (tiles(256, 256) >= 192) {
-      c.bm = 256, c.bn = 256, c.bk = 64;
-    } else if (tiles(128, 128) >= 128) {
-      c.bm = 128, c.bn = 128, c.bk = 64;
-    } else {
-      c.bm = 64, c.bn = 64, c.bk = 64;
+    int t = ForcedHalfTile();
+    if (t < 0) {
+      // Rounds of resident tiles on the 256 CUs: one 256x256 tile (8
+      // waves) per CU, two 128x128 tiles per CU. Measured on MI355X, a
+      // round of 128x128 tiles costs ~0.6 of a round of 256x256 tiles.
+      const int cus = DeviceComputeUnits();
+      const double r256 = static_cast<double>(CeilDiv(tiles(256, 256), cus));
+      const double r128 =
+          0.6 * static_cast<double>(CeilDiv(tiles(128, 128), 2 * cus));
+      if (tiles(128, 128) < cus)
+        t = 3;  // too little work for 128x128 tiles to fill the GPU
+      else
+        t = r256 <= r128 ? 1 : 2;
     }
+    c.tile = t;
+    c.bm = kHalfTiles[t].bm, c.bn = kHalfTiles[t].bn, c.bk = 64;
   } else {
     if (tiles(128, 128) >= 192) {
       c.bm = 128, c.bn = 128, c.bk = 32;
@@ -390,11 +703,33 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
       c.bm = 64, c.bn = 64, c.bk = 32;
     }
   }
-  c.name = std::string("gemm_mfma_") + DTypeName(p.a.dtype) + "_" +
-           std::to_string(c.bm) + "x" + std::to_string(c.bn) + "x" +
-           std::to_string(c.bk) + (p.a.transpose ? "_t" : "_n") +
-           (p.b.transpose ? "t" : "n");
+  c.name = std::string(half ? "gemm_tile_" : "gemm_mfma_") +
+           DTypeName(p.a.dtype) + "_" + std::to_string(c.bm) + "x" +
+           std::to_string(c.bn) + "x" + std::to_string(c.bk) +
+           (half ? "_w" + std::to_string(kHalfTiles[c.tile].wm *
+                                         kHalfTiles[c.tile].wn)
+                 : std::string()) +
+           (p.a.transpose ? "_t" : "_n") + (p.b.transpose ? "t" : "n");
   return c;
+}
+
+template <typename T>
+qk_status DispatchHalf(int tile, const GemmArgs& g, int batch, bool ta,
+                       bool tb, hipStream_t st, const char* name) {
+  switch (tile) {
+    case 0:
+      return DispatchTile<T, 256, 256, 64, 2, 2>(g, batch, ta, tb, st, name);
+    case 1:
+      return DispatchTile<T, 256, 256, 64, 2, 4>(g, batch, ta, tb, st, name);
+    case 2:
+      return DispatchTile<T, 128, 128, 64, 2, 2>(g, batch, ta, tb, st, name);
+    case 4:
+      return DispatchTile<T, 256, 128, 64, 2, 2>(g, batch, ta, tb, st, name);
+    case 5:
+      return DispatchTile<T, 128, 256, 64, 2, 2>(g, batch, ta, tb, st, name);
+    default:
+      return DispatchTile<T, 64, 64, 64, 2, 2>(g, batch, ta, tb, st, name);
+  }
 }
 
 qk_status LaunchGemm(const GemmProblem& p, hipStream_t stream) {
@@ -429,6 +764,8 @@ qk_status LaunchGemm(const GemmProblem& p, hipStream_t stream) {
     return (reinterpret_cast<uintptr_t>(o.ptr) % 16 == 0) && o.ld % vec == 0 &&
            bs % vec == 0;
   };
+  g.out_vec = (reinterpret_cast<uintptr_t>(p.d.ptr) % 16 == 0) &&
+              p.d.ld % 4 == 0 && g.bsd % 4 == 0;
   g.a_vec = vec_ok(p.a, g.bsa);
   g.b_vec = vec_ok(p.b, g.bsb);
   g.tiles_m = static_cast<int>(CeilDiv(p.m, c.bm));
@@ -446,17 +783,9 @@ qk_status LaunchGemm(const GemmProblem& p, hipStream_t stream) {
   const char* name = c.name.c_str();
   switch (p.a.dtype) {
     case QK_BF16:
-      if (c.bm == 256)
-        return Dispatch<bf16, 256, 256, 64, 2, 4>(g, batch, ta, tb, stream, name);
-      if (c.bm == 128)
-        return Dispatch<bf16, 128, 128, 64, 2, 2>(g, batch, ta, tb, stream, name);
-      return Dispatch<bf16, 64, 64, 64, 2, 2>(g, batch, ta, tb, stream, name);
+      return DispatchHalf<bf16>(c.tile, g, batch, ta, tb, stream, name);
     case QK_F16:
-      if (c.bm == 256)
-        return Dispatch<f16, 256, 256, 64, 2, 4>(g, batch, ta, tb, stream, name);
-      if (c.bm == 128)
-        return Dispatch<f16, 128, 128, 64, 2, 2>(g, batch, ta, tb, stream, name);
-      return Dispatch<f16, 64, 64, 64, 2, 2>(g, batch, ta, tb, stream, name);
+      return DispatchHalf<f16>(c.tile, g, batch, ta, tb, stream, name);
     default:
       if (c.bm == 128)
         return Dispatch<float, 128, 128, 32, 2, 2>(g, batch, ta, tb, stream, name);

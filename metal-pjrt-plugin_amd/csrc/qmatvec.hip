@@ -26,6 +26,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <string>
+#include <type_traits>
 
 #include "qk_device.h"
 #include "qk_internal.h"
@@ -461,7 +462,15 @@ __device__ __forceinline__ float ChunkDot(const u32x4& w, const u32x4* xq,
   return d;
 }
 
-template <int PACK, typename XT, int MT, int CPL>
+// Scale/offset element i: bf16 (the common case, no dtype branch) or any
+// float type chosen at run time.
+template <bool kBf16SB>
+__device__ __forceinline__ float LoadSB(const void* p, long long i, int dt) {
+  if constexpr (kBf16SB) return to_f32(static_cast<const bf16*>(p)[i]);
+  return load_any(p, i, dt);
+}
+
+template <int PACK, typename XT, int MT, int CPL, bool kBf16SB>
 __global__ __launch_bounds__(kStreamThreads) void qmv_stream_kernel(
     QmvArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -473,6 +482,9 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_stream_kernel(
   const int GW = gridDim.x * (kStreamThreads / 64);
   const int groups = a.k / a.group;
   constexpr bool kInt4 = ChunkTraits<PACK>::kInt4;
+  // Rows in flight per wave: D slots, D - 1 of them loading while one is
+  // computed.
+  constexpr int D = CPL <= 2 ? 4 : (CPL <= 4 ? 3 : 2);
 
   // Codes, scales and offsets of one row for this lane's chunks.
   struct RowRegs {
@@ -489,21 +501,12 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_stream_kernel(
         int kb, grp;
         ChunkSpan<PACK>(c, a.group, &kb, &grp);
         const long long gi = static_cast<long long>(row) * groups + grp;
-        r.s[j] = load_any(a.scales, gi, a.sdt);
-        r.b[j] = a.has_bias ? load_any(a.biases, gi, a.bdt) : 0.f;
+        r.s[j] = LoadSB<kBf16SB>(a.scales, gi, a.sdt);
+        r.b[j] = a.has_bias ? LoadSB<kBf16SB>(a.biases, gi, a.bdt) : 0.f;
       }
     }
   };
-
-  RowRegs cur, nxt;
-  int row = gw;
-  if (row < a.n) load_row(row, cur);  // in flight while x is staged
-  StageX<PACK, XT>(a, a.m, cpr, xq, xs);
-  __syncthreads();
-
-  for (; row < a.n; row += GW) {
-    const int nrow = row + GW;
-    if (nrow < a.n) load_row(nrow, nxt);
+  auto compute_row = [&](int row, const RowRegs& r) {
     float acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0.f;
@@ -512,12 +515,12 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_stream_kernel(
       const int c = lane + 64 * j;
       if (c >= cpr) continue;
       // 4-bit codes carry +128 (see ChunkDot): fold it into the offset.
-      const float boff = kInt4 ? cur.b[j] - 128.f * cur.s[j] : cur.b[j];
+      const float boff = kInt4 ? r.b[j] - 128.f * r.s[j] : r.b[j];
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         if (m >= a.m) break;
-        const float d = ChunkDot<PACK>(cur.w[j], xq, m, cpr, c);
-        acc[m] = fmaf(cur.s[j], d, fmaf(boff, xs[m * cpr + c], acc[m]));
+        const float d = ChunkDot<PACK>(r.w[j], xq, m, cpr, c);
+        acc[m] = fmaf(r.s[j], d, fmaf(boff, xs[m * cpr + c], acc[m]));
       }
     }
 #pragma unroll
@@ -528,11 +531,30 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_stream_kernel(
         static_cast<XT*>(a.y)[static_cast<long long>(m) * a.n + row] =
             from_f32<XT>(v);
     }
-    cur = nxt;
+  };
+
+  RowRegs buf[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int r = gw + d * GW;
+    if (r < a.n) load_row(r, buf[d]);  // in flight while x is staged
+  }
+  StageX<PACK, XT>(a, a.m, cpr, xq, xs);
+  __syncthreads();
+
+  for (int row = gw; row < a.n; row += D * GW) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int r = row + d * GW;
+      if (r >= a.n) break;
+      compute_row(r, buf[d]);
+      const int nr = r + D * GW;
+      if (nr < a.n) load_row(nr, buf[d]);
+    }
   }
 }
 
-template <int PACK, typename XT, int MT>
+template <int PACK, typename XT, int MT, bool kBf16SB>
 qk_status LaunchStreamMT(QmvArgs a, int cpl, int cus, hipStream_t st) {
   const int cpr = a.row_bytes / 16;
   const size_t lds = static_cast<size_t>(MT) * cpr * (64 + 4);
@@ -549,17 +571,15 @@ qk_status LaunchStreamMT(QmvArgs a, int cpl, int cus, hipStream_t st) {
   };
   switch (cpl) {
     case 1:
-      return go(qmv_stream_kernel<PACK, XT, MT, 1>);
+      return go(qmv_stream_kernel<PACK, XT, MT, 1, kBf16SB>);
     case 2:
-      return go(qmv_stream_kernel<PACK, XT, MT, 2>);
-    case 3:
-      return go(qmv_stream_kernel<PACK, XT, MT, 3>);
+      return go(qmv_stream_kernel<PACK, XT, MT, 2, kBf16SB>);
     case 4:
-      return go(qmv_stream_kernel<PACK, XT, MT, 4>);
+      return go(qmv_stream_kernel<PACK, XT, MT, 4, kBf16SB>);
     case 6:
-      return go(qmv_stream_kernel<PACK, XT, MT, 6>);
+      return go(qmv_stream_kernel<PACK, XT, MT, 6, kBf16SB>);
     default:
-      return go(qmv_stream_kernel<PACK, XT, MT, 8>);
+      return go(qmv_stream_kernel<PACK, XT, MT, 8, kBf16SB>);
   }
 }
 
@@ -570,17 +590,26 @@ bool LaunchStream(const QmvArgs& a, int cus, hipStream_t stream,
   const int cpr = a.row_bytes / 16;
   int cpl = (cpr + 63) / 64;
   if (cpl > 8 || a.m > 4) return false;
+  if (cpl == 3) cpl = 4;
   if (cpl == 5) cpl = 6;
   if (cpl == 7) cpl = 8;
-  const int mt = a.m <= 1 ? 1 : a.m <= 2 ? 2 : 4;
+  // The decode case (bf16 x, bf16 scales) gets kernels per row count;
+  // everything else runs the four-row kernel with masked rows.
+  const bool sb16 = a.sdt == QK_BF16 && (!a.has_bias || a.bdt == QK_BF16);
+  const bool fast = sb16 && std::is_same<XT, bf16>::value;
+  const int mt = !fast ? 4 : a.m <= 1 ? 1 : a.m <= 2 ? 2 : 4;
   const size_t lds = static_cast<size_t>(mt) * cpr * (64 + 4);
   if (lds > 64 * 1024) return false;
-  if (mt == 1)
-    *st = LaunchStreamMT<PACK, XT, 1>(a, cpl, cus, stream);
-  else if (mt == 2)
-    *st = LaunchStreamMT<PACK, XT, 2>(a, cpl, cus, stream);
-  else
-    *st = LaunchStreamMT<PACK, XT, 4>(a, cpl, cus, stream);
+  if (fast) {
+    if (mt == 1)
+      *st = LaunchStreamMT<PACK, XT, 1, true>(a, cpl, cus, stream);
+    else if (mt == 2)
+      *st = LaunchStreamMT<PACK, XT, 2, true>(a, cpl, cus, stream);
+    else
+      *st = LaunchStreamMT<PACK, XT, 4, true>(a, cpl, cus, stream);
+  } else {
+    *st = LaunchStreamMT<PACK, XT, 4, false>(a, cpl, cus, stream);
+  }
   return true;
 }
 

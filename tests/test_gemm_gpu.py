@@ -160,8 +160,9 @@ def test_leading_dim_padding(dev, ta, tb):
 
 @pytest.mark.parametrize("shape,kernel", [
     ((97, 160, 72), "64x64"),
-    ((1536, 1536, 72), "128x128"),
-    ((3584, 3584, 40), "256x256"),
+    ((1536, 1536, 72), "64x64"),
+    ((2048, 12288, 40), "128x128"),
+    ((4096, 4096, 40), "256x256"),
 ])
 def test_all_tile_configs(dev, shape, kernel):
     for ta in (False, True):
