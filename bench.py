@@ -12,9 +12,11 @@ Also reported (`secondary`): bf16 GEMM + bias + SiLU TFLOP/s at the C3
 shapes (the metric's second half), int4 M = 16 / 512, int8 affine GEMV,
 RMSNorm and softmax [4096, 4096] HBM GB/s; each against its roofline.
 
-Timing: HIP events recorded on the stream the kernels are launched on
-(torch's current stream, which qkern launches on), W untimed warm-up steps,
-then K timed steps bracketed by torch.cuda.synchronize().
+Timing: the W warm-up steps and the K timed steps are each captured into a
+HIP graph (the launches only: outputs are preallocated, nothing is
+allocated or cleared inside); the timed graph is replayed once between two
+HIP events on the replaying stream, bracketed by torch.cuda.synchronize().
+Wall-clock time over the same region gives `value`.
 
 CPU baseline: the oracle's C port of the reference's _matvec_int4
 (oracle/qk_oracle.c, float32, OpenMP over output rows) on the host cores,
@@ -56,17 +58,34 @@ def make_int4(torch, dev, n, k, gen):
     return words, s, b
 
 
+def capture(torch, fn, iters):
+    """A HIP graph of fn(0), ..., fn(iters - 1) (pure kernel launches: no
+    allocation, memset or host synchronization inside)."""
+    fn(0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(iters):
+                fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    return g
+
+
 def timed_launches(torch, fn, iters):
     """Average device time (ms) per call of fn over `iters` back-to-back
-    calls, from two HIP events on the current stream (the stream qkern
-    launches on) around all of them."""
-    fn(0)
+    calls replayed from a HIP graph, from two HIP events recorded on the
+    replaying stream around the replay (after one untimed replay)."""
+    g = capture(torch, fn, iters)
+    g.replay()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record()
-    for i in range(iters):
-        fn(i)
+    g.replay()
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / iters
@@ -228,17 +247,18 @@ def main():
         for j in range(len(QWEN3_8B)):
             qkern.qmatvec(xs[j], *ws[j], out=ys[j])
 
-    for i in range(args.warmup):
-        step(i)
-    # Timed region: K steps, HIP events on the launch stream at both ends
-    # (no events between launches), bracketed by device synchronization.
+    # The K timed steps are captured into one HIP graph (so host launch
+    # overhead does not leave the GPU idle between the short kernels), the
+    # warm-up steps into another; both replay on one stream.
+    warm = capture(torch, step, max(args.warmup, 1))
+    timed = capture(torch, step, args.steps)
+    warm.replay()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record()
-    for i in range(args.steps):
-        step(i)
+    timed.replay()
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -257,7 +277,7 @@ def main():
         shapes.append({"n": n, "k": k, "us": round(ms * 1e3, 2),
                        "gbs": round(per_shape_bytes[j] / (ms * 1e-3) / 1e9,
                                     1)})
-    del sets
+    del warm, timed, sets
 
     result = {
         "metric": "int4 GEMV HBM GB/s (% of peak); bf16 GEMM TFLOP/s "

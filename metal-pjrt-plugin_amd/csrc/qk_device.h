@@ -72,6 +72,37 @@ __device__ __forceinline__ float act_f32(int act, float x) {
   return x;
 }
 
+// A 32-bit constant held in a VGPR. gfx9 VOP3 instructions (v_and_or_b32,
+// v_bfi_b32, ...) take no literal operand and at most one SGPR, so a
+// literal mask used by them would be split into two VOP2 instructions.
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
+  return r;
+}
+
+// Sum over the 64 lanes of a wavefront with DPP row operations (quad
+// swaps, half-row and row mirrors) and four lane reads; the result is
+// wave-uniform.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl,
+                                         0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror
+  v += dpp_f32<0x140>(v);  // row_mirror: every lane holds its row's sum
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 // Sum / max over the 64 lanes of a wavefront; every lane gets the result.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -554,6 +554,139 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_stream_kernel(
   }
 }
 
+// The decode hot path: M = 1, bf16 x, 4-bit codes, group size 64, bf16
+// scales/offsets, rows whose 16-byte chunks split evenly over the 64 lanes
+// in pairs. Lane l owns the groups l, l + 64, ... (two chunks each), so it
+// loads one scale and one offset per group and a wave's loads stay
+// contiguous across lanes. x is held in registers
+// (a lane's chunks are the same for every row); codes become (128 + q)
+// bf16 pairs with one v_and_or_b32 each; rows are reduced with DPP.
+template <int PACK, int CPL>
+__global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int cpr = 64 * CPL;
+  constexpr int G = CPL / 2;  // groups per lane
+  u32x4* xq = reinterpret_cast<u32x4*>(smem);
+  float* xs_lds = reinterpret_cast<float*>(smem + 4 * cpr * 16);
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * (kStreamThreads / 64) + (threadIdx.x >> 6);
+  const int GW = gridDim.x * (kStreamThreads / 64);
+  constexpr int D = CPL <= 2 ? 4 : (CPL <= 4 ? 3 : 2);
+  constexpr int groups = cpr / 2;
+
+  const uint8_t* cbase = a.codes + lane * 32;
+  const bf16* S = static_cast<const bf16*>(a.scales) + lane;
+  const bf16* Bo = static_cast<const bf16*>(a.biases) + lane;
+
+  struct Slot {
+    u32x4 w[CPL];
+    float s[G], b[G];
+  };
+  auto load_row = [&](int row, Slot& r) {
+    const uint8_t* p = cbase + static_cast<long long>(row) * a.row_bytes;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)  // chunk j: group j/2, half j%2
+      r.w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+          p + 2048 * (j >> 1) + 16 * (j & 1)));
+    const long long gb = static_cast<long long>(row) * groups;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      r.s[h] = to_f32(S[gb + 64 * h]);
+      r.b[h] = a.has_bias ? to_f32(Bo[gb + 64 * h]) : 0.f;
+    }
+  };
+
+  Slot buf[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int r = gw + d * GW;
+    if (r < a.n) load_row(r, buf[d]);  // in flight while x is staged
+  }
+  StageX<PACK, bf16>(a, 1, cpr, xq, xs_lds);
+  __syncthreads();
+  u32x4 xr[CPL][4];
+  float xsum[G];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = 2 * (lane + 64 * (j >> 1)) + (j & 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xr[j][i] = xq[i * cpr + c];
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const int c = 2 * (lane + 64 * h);
+    xsum[h] = xs_lds[c] + xs_lds[c + 1];
+  }
+  const uint32_t kMask = vgpr_const(0x000F000Fu);
+  const uint32_t kBias = vgpr_const(0x43004300u);
+
+  auto compute_row = [&](int row, const Slot& r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float d = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * h + jj;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t word = r.w[j][i];
+#pragma unroll
+          for (int sh = 0; sh < 4; ++sh) {
+            const uint32_t cp = ((word >> (4 * sh)) & kMask) | kBias;
+            const uint32_t xp = xr[j][i][sh];
+            d = __builtin_amdgcn_fdot2_f32_bf16(AsBf16x2(cp), AsBf16x2(xp), d,
+                                                false);
+          }
+        }
+      }
+      acc = fmaf(r.s[h], d, fmaf(r.b[h] - 128.f * r.s[h], xsum[h], acc));
+    }
+    const float v = wave_sum_dpp(acc);
+    if (lane == 0) static_cast<bf16*>(a.y)[row] = from_f32<bf16>(v);
+  };
+
+  for (int row = gw; row < a.n; row += D * GW) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int r = row + d * GW;
+      if (r >= a.n) break;
+      compute_row(r, buf[d]);
+      const int nr = r + D * GW;
+      if (nr < a.n) load_row(nr, buf[d]);
+    }
+  }
+}
+
+template <int PACK>
+bool LaunchM1(const QmvArgs& a, int cus, hipStream_t stream, qk_status* st) {
+  const int cpr = a.row_bytes / 16;
+  if (a.m != 1 || a.group != 64 || cpr % 128 != 0) return false;
+  const int cpl = cpr / 64;
+  const size_t lds = static_cast<size_t>(cpr) * (64 + 4);
+  const int need = (a.n + 3) / 4;
+  auto go = [&](auto kernel) {
+    const int per_cu = ResidentBlocks(reinterpret_cast<const void*>(kernel),
+                                      kStreamThreads, lds);
+    const int grid = std::max(1, std::min(need, cus * per_cu));
+    kernel<<<grid, kStreamThreads, lds, stream>>>(a);
+    *st = PostLaunch("qmv_m1");
+    return true;
+  };
+  switch (cpl) {
+    case 2:
+      return go(qmv_m1_kernel<PACK, 2>);
+    case 4:
+      return go(qmv_m1_kernel<PACK, 4>);
+    case 6:
+      return go(qmv_m1_kernel<PACK, 6>);
+    case 8:
+      return go(qmv_m1_kernel<PACK, 8>);
+    default:
+      return false;
+  }
+}
+
 template <int PACK, typename XT, int MT, bool kBf16SB>
 qk_status LaunchStreamMT(QmvArgs a, int cpl, int cus, hipStream_t st) {
   const int cpr = a.row_bytes / 16;
@@ -600,6 +733,10 @@ bool LaunchStream(const QmvArgs& a, int cus, hipStream_t stream,
   const int mt = !fast ? 4 : a.m <= 1 ? 1 : a.m <= 2 ? 2 : 4;
   const size_t lds = static_cast<size_t>(mt) * cpr * (64 + 4);
   if (lds > 64 * 1024) return false;
+  if (fast && a.m == 1 && ChunkTraits<PACK>::kInt4 && lds <= 64 * 1024 &&
+      LaunchM1<PACK>(a, cus, stream, st)) {
+    return true;
+  }
   if (fast) {
     if (mt == 1)
       *st = LaunchStreamMT<PACK, XT, 1, true>(a, cpl, cus, stream);
