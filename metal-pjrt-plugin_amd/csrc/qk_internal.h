@@ -92,6 +92,10 @@ struct QuantProblem {
 };
 
 qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream);
+
+// Dequantizing MFMA GEMM (qgemm.hip) for more than four rows of x.
+bool QGemmApplies(const QuantProblem& p);
+qk_status LaunchQGemm(const QuantProblem& p, hipStream_t stream);
 qk_status LaunchDequantize(const QuantProblem& p, hipStream_t stream);
 
 // ---------------------------------------------------------------------------

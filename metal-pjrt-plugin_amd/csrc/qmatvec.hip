@@ -839,6 +839,10 @@ qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream) {
   }
   QmvArgs a = MakeArgs(p);
   const int m = static_cast<int>(p.m);
+  // Beyond four rows, like the reference's linear() (ROWS_MAX = 4,
+  // examples/llm/qwen3.py:215-230): dequantize to x's type and multiply,
+  // fused into one MFMA GEMM.
+  if (m > 4 && QGemmApplies(p)) return LaunchQGemm(p, stream);
   if (m <= 4) {
     const int cus = DeviceComputeUnits();
     qk_status st = QK_OK;
