@@ -58,6 +58,23 @@ def make_int4(torch, dev, n, k, gen):
     return words, s, b
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles",
+                               "int4_gemv_qwen3_8b_decode.md")
+
+
+def profiled_traffic():
+    """HBM bytes per launch of the headline kernel, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (None when absent)."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def capture(torch, fn, iters):
     """A HIP graph of fn(0), ..., fn(iters - 1) (pure kernel launches: no
     allocation, memset or host synchronization inside)."""
@@ -219,6 +236,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 10 plain device copies of 512 MiB (the "
+                         "reference kernel for FETCH_SIZE/WRITE_SIZE scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -231,6 +251,15 @@ def main():
     import qkern.blas  # noqa: F401
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.ones(128 * 1024 * 1024, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 4,
+                          "copy_bytes_written": dst.numel() * 4}))
+        return
     gen = torch.Generator(device=dev).manual_seed(0)
     rot = 3
     sets = [[make_int4(torch, dev, n, k, gen) for (n, k) in QWEN3_8B]
@@ -304,8 +333,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
-                     "kernel": "qmv_stream_kernel (algorithmic bytes / "
+                     "traffic": profiled_traffic(),
+                     "traffic_unit": "bytes per launch (profiles/"
+                                     "int4_gemv_qwen3_8b_decode.md)",
+                     "kernel": "qmv_m1_kernel (algorithmic bytes / "
                                "device time, over the 4 launches of each "
                                "timed step)"},
     }
