@@ -267,6 +267,21 @@ qk_status DispatchTile(const GemmArgs& g, int batch, bool ta, bool tb,
   return PostLaunch(name);
 }
 
+template <typename T, int BN>
+qk_status DispatchFast(const GemmArgs& g, int batch, bool ta, bool tb,
+                       hipStream_t stream, const char* name) {
+  dim3 grid(g.tiles_m * g.tiles_n, batch);
+  if (!ta && !tb)
+    gemm_fast_kernel<T, BN, false, false><<<grid, 256, 0, stream>>>(g);
+  else if (!ta && tb)
+    gemm_fast_kernel<T, BN, false, true><<<grid, 256, 0, stream>>>(g);
+  else if (ta && !tb)
+    gemm_fast_kernel<T, BN, true, false><<<grid, 256, 0, stream>>>(g);
+  else
+    gemm_fast_kernel<T, BN, true, true><<<grid, 256, 0, stream>>>(g);
+  return PostLaunch(name);
+}
+
 struct TileCfg {
   int bm, bn, bk, wm, wn;
 };
@@ -306,7 +321,10 @@ constexpr HalfTile kHalfTiles[] = {
     {64, 64, 2, 2},    // 3
     {256, 128, 2, 2},  // 4
     {128, 256, 2, 2},  // 5
+    {256, 256, 2, 2},  // 6: interior-tile kernel (gemm_fast_kernel)
+    {256, 128, 2, 2},  // 7: interior-tile kernel, 128 x 64 per wave
 };
+constexpr int kFastTile256 = 6, kFastTile128 = 7;
 constexpr int kNumHalfTiles = sizeof(kHalfTiles) / sizeof(kHalfTiles[0]);
 
 // QK_GEMM_TILE=<index into kHalfTiles> forces a configuration (tuning).
@@ -320,6 +338,25 @@ int ForcedHalfTile() {
   return forced;
 }
 
+// Whether the interior-tile kernel can run the problem with a BN-wide
+// tile: M, N, K multiples of the tile, 16-byte aligned operands and leading
+// dimensions, and each operand of one batch entry under 2^31 bytes (the
+// extent of a buffer descriptor).
+bool FastApplies(const GemmProblem& p, int bn) {
+  if (p.a.dtype == QK_F32 || p.m % 256 != 0 || p.n % bn != 0 ||
+      p.k % 64 != 0 || p.k == 0)
+    return false;
+  const int vec = 16 / DTypeSize(p.a.dtype);
+  const bool batched = p.batch > 1;
+  auto ok = [&](const Operand& o, int64_t rows) {
+    const int64_t bs = batched ? o.batch_stride : 0;
+    return reinterpret_cast<uintptr_t>(o.ptr) % 16 == 0 && o.ld % vec == 0 &&
+           bs % vec == 0 && rows * o.ld * DTypeSize(o.dtype) < (int64_t{1} << 31);
+  };
+  return ok(p.a, p.a.transpose ? p.k : p.m) &&
+         ok(p.b, p.b.transpose ? p.n : p.k);
+}
+
 GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
   GemmKernelChoice c;
   const bool half = p.a.dtype != QK_F32;
@@ -329,11 +366,22 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
   };
   if (half) {
     int t = ForcedHalfTile();
+    if ((t == kFastTile256 && !FastApplies(p, 256)) ||
+        (t == kFastTile128 && !FastApplies(p, 128)))
+      t = -1;
+    const int cus = DeviceComputeUnits();
+    if (t < 0 && FastApplies(p, 128) && tiles(256, 128) >= cus / 2) {
+      // One 256-row tile per CU. Measured on MI355X, a round of 256x128
+      // tiles costs ~0.67 of a round of 256x256 tiles.
+      const double r256 = static_cast<double>(CeilDiv(tiles(256, 256), cus));
+      const double r128 =
+          0.67 * static_cast<double>(CeilDiv(tiles(256, 128), cus));
+      t = FastApplies(p, 256) && r256 <= r128 ? kFastTile256 : kFastTile128;
+    }
     if (t < 0) {
       // Rounds of resident tiles on the 256 CUs: one 256x256 tile (8
       // waves) per CU, two 128x128 tiles per CU. Measured on MI355X, a
       // round of 128x128 tiles costs ~0.6 of a round of 256x256 tiles.
-      const int cus = DeviceComputeUnits();
       const double r256 = static_cast<double>(CeilDiv(tiles(256, 256), cus));
       const double r128 =
           0.6 * static_cast<double>(CeilDiv(tiles(128, 128), 2 * cus));
@@ -351,7 +399,8 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
       c.bm = 64, c.bn = 64, c.bk = 32;
     }
   }
-  c.name = std::string(half ? "gemm_tile_" : "gemm_mfma_") +
+  const bool fast = half && c.tile >= kFastTile256;
+  c.name = std::string(!half ? "gemm_mfma_" : fast ? "gemm_fast_" : "gemm_tile_") +
            DTypeName(p.a.dtype) + "_" + std::to_string(c.bm) + "x" +
            std::to_string(c.bn) + "x" + std::to_string(c.bk) +
            (half ? "_w" + std::to_string(kHalfTiles[c.tile].wm *
@@ -375,6 +424,10 @@ qk_status DispatchHalf(int tile, const GemmArgs& g, int batch, bool ta,
       return DispatchTile<T, 256, 128, 64, 2, 2>(g, batch, ta, tb, st, name);
     case 5:
       return DispatchTile<T, 128, 256, 64, 2, 2>(g, batch, ta, tb, st, name);
+    case kFastTile256:
+      return DispatchFast<T, 256>(g, batch, ta, tb, st, name);
+    case kFastTile128:
+      return DispatchFast<T, 128>(g, batch, ta, tb, st, name);
     default:
       return DispatchTile<T, 64, 64, 64, 2, 2>(g, batch, ta, tb, st, name);
   }

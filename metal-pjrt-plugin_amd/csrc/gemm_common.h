@@ -243,6 +243,121 @@ struct DenseB {
   __device__ __forceinline__ void store(T* lds) const { ld.store(lds, tid); }
 };
 
+// Four consecutive output-type elements as f32 (vector load when `vec`).
+template <typename T>
+__device__ __forceinline__ void ld_out4(const void* p, long long i, bool f32,
+                                        bool vec, int cnt, float (&v)[4]) {
+  if (vec && cnt == 4) {
+    if (f32) {
+      const float4 q = *reinterpret_cast<const float4*>(
+          static_cast<const float*>(p) + i);
+      v[0] = q.x, v[1] = q.y, v[2] = q.z, v[3] = q.w;
+    } else {
+      union {
+        u32x2 u;
+        T e[4];
+      } q;
+      q.u = *reinterpret_cast<const u32x2*>(static_cast<const T*>(p) + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = to_f32(q.e[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = e < cnt ? ld_out<T>(p, i + e, f32) : 0.f;
+  }
+}
+template <typename T>
+__device__ __forceinline__ void st_out4(void* p, long long i, bool f32,
+                                        bool vec, int cnt, const float (&v)[4]) {
+  if (vec && cnt == 4) {
+    if (f32) {
+      *reinterpret_cast<float4*>(static_cast<float*>(p) + i) =
+          make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      union {
+        u32x2 u;
+        T e[4];
+      } o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o.e[e] = from_f32<T>(v[e]);
+      *reinterpret_cast<u32x2*>(static_cast<T*>(p) + i) = o.u;
+    }
+  } else {
+    for (int e = 0; e < cnt; ++e) st_out<T>(p, i + e, f32, v[e]);
+  }
+}
+
+// Epilogue through LDS, one slab of WTM output rows (one row of waves) at
+// a time: the waves of that row write their f32 accumulators, then all
+// threads apply alpha, beta*C, bias, aux and the activation to four
+// consecutive columns each and store them with one vector store. Each
+// thread keeps the same four columns for the whole tile, so it loads its
+// bias once. `lds` holds at least WTM x (BN + 4) floats; the caller has
+// synchronised after its last use of it.
+template <typename T, int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_tile(
+    const GemmArgs& g, const f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
+    unsigned char* lds, int m0, int n0, long long batch, int tid) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int kLdo = BN + 4;  // f32 staging row stride
+  constexpr int kQuads = BN / 4;  // column quads per row
+  static_assert(NT % kQuads == 0, "a thread's columns must not move");
+  constexpr int kRowStep = NT / kQuads;  // rows between a thread's quads
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const bool of32 = g.out_f32 != 0;
+  const bool vec = g.out_vec != 0;
+  const long long dbase = batch * g.bsd;
+  float* stage = reinterpret_cast<float*>(lds);
+  const int lc = (tid % kQuads) * 4, lr0 = tid / kQuads;
+  const int col = n0 + lc;
+  const int cnt = max(0, min(4, g.n - col));
+  float bias[4] = {0.f, 0.f, 0.f, 0.f};
+  if (g.has_bias && cnt > 0) ld_out4<T>(g.bias, col, of32, false, cnt, bias);
+#pragma unroll 1
+  for (int slab = 0; slab < WM; ++slab) {
+    if (wm == slab) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int c = wn * WTN + j * 32 + (lane & 31);
+            stage[row * kLdo + c] = acc[i][j][r];
+          }
+    }
+    __syncthreads();
+    if (cnt > 0) {
+#pragma unroll 4
+      for (int lr = lr0; lr < WTM; lr += kRowStep) {
+        const int row = m0 + slab * WTM + lr;
+        if (row >= g.m) break;
+        const float4 a4 =
+            *reinterpret_cast<const float4*>(stage + lr * kLdo + lc);
+        float v[4] = {a4.x, a4.y, a4.z, a4.w};
+        const long long idx = dbase + static_cast<long long>(row) * g.ldd + col;
+        float c4[4] = {0.f, 0.f, 0.f, 0.f};
+        if (g.use_c) ld_out4<T>(g.c, idx, of32, vec, cnt, c4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = g.alpha * v[e];
+          if (g.use_c) v[e] += g.beta * c4[e];
+          if (g.has_bias) v[e] += bias[e];
+        }
+        if (g.has_aux) st_out4<T>(g.aux, idx, of32, vec, cnt, v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = act_f32(g.act, v[e]);
+        st_out4<T>(g.d, idx, of32, vec, cnt, v);
+      }
+    }
+    __syncthreads();
+  }
+}
+
 template <typename T, int BM, int BN, int BK, int WM, int WN, bool TA, class BSrc>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs g) {
   constexpr int NT = WM * WN * 64;
@@ -334,66 +449,186 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs g) {
     __syncthreads();
   }
 
-  // Epilogue through LDS, one slab of WTM output rows (one row of waves)
-  // at a time: the waves of that row write their f32 accumulators, then
-  // all threads apply alpha, beta*C, bias, aux and the activation to four
-  // consecutive columns each and store them with one vector store.
-  const bool of32 = g.out_f32 != 0;
-  const long long dbase = batch * g.bsd;
-  float* stage = reinterpret_cast<float*>(lds_raw);
-  const bool vec_out = g.out_vec != 0;
-#pragma unroll 1
-  for (int slab = 0; slab < WM; ++slab) {
-    if (wm == slab) {
+  // The K loop ends on a barrier, so the tile stages are free.
+  store_tile<T, BM, BN, WM, WN>(g, acc, lds_raw, m0, n0, batch, tid);
+}
+
+
+// ---------------------------------------------------------------------------
+// Interior-tile f16/bf16 kernel for problems whose M, N and K are multiples
+// of the tile (BM = 256, BN = 256 or 128, BK = 64) and whose operands allow
+// 16-byte loads: no bounds checks in the K loop.
+//
+//  - Four waves (2 x 2), each owning a 128 x BN/2 block of D: 16 (or 8)
+//    32x32 accumulators, so one wave per SIMD keeps every MFMA pipe fed.
+//  - Global loads are raw buffer loads: one descriptor per operand, one
+//    VGPR byte offset per thread and an SGPR offset per vector, so the
+//    address arithmetic of the loads is scalar.
+//  - The next K tile is in registers during the whole current tile; it is
+//    written to the other LDS stage in the last 16-wide K step, its DS
+//    writes interleaved one per MFMA; the tile after it is requested right
+//    after the barrier, so every global load has one tile of MFMA time to
+//    land.
+//  - MFMA fragments are double-buffered in registers: the DS reads for
+//    K step s + 1 are issued between the MFMAs of step s, one per MFMA
+//    (sched_group_barrier), so LDS latency hides under the matrix pipe.
+//
+// Buffer descriptors take a 32-bit extent, so each operand of one batch
+// entry must span less than 2^31 bytes (checked by the launcher).
+template <typename T, int R, int BK, int NT, bool KCONT>
+struct BufferLoader {
+  static constexpr int VPR = (KCONT ? BK : R) / 8;  // vectors per source row
+  static constexpr int RPI = NT / VPR;  // source rows between vector slots
+  static constexpr int NV = R * BK / 8 / NT;
+  static_assert(NT % VPR == 0 && NV * NT * 8 == R * BK, "bad tile split");
+  __amdgpu_buffer_rsrc_t rsrc;
+  int voff;  // bytes
+  int ld;    // elements
+  u32x4 v[NV];
+  __device__ __forceinline__ void init(const T* src, long long bytes, int ld_,
+                                       int tid) {
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(src), (short)0,
+                                             static_cast<int>(bytes),
+                                             0x00020000);
+    ld = ld_;
+    voff = ((tid / VPR) * ld + (tid % VPR) * 8) * static_cast<int>(sizeof(T));
+  }
+  // Tile origin: rows r0 (M or N), k0.
+  __device__ __forceinline__ void load(int r0, int k0) {
+    const int base = KCONT ? r0 * ld + k0 : k0 * ld + r0;  // elements
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int soff = (base + i * RPI * ld) * static_cast<int>(sizeof(T));
+      v[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, 0);
+    }
+  }
+  __device__ __forceinline__ void store(T* lds, int tid) const {
+    constexpr int LD = TileLayout<T, R, BK, KCONT>::kLd;
+    T* p = lds + (tid / VPR) * LD + (tid % VPR) * 8;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      *reinterpret_cast<u32x4*>(p + i * RPI * LD) = v[i];
+  }
+};
+
+template <typename T, int BN, bool TA, bool TB>
+__global__ __launch_bounds__(256) void gemm_fast_kernel(GemmArgs g) {
+  constexpr int BM = 256, BK = 64, NT = 256, WM = 2, WN = 2;
+  constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
+  constexpr bool AK = !TA, BKC = TB;  // K-contiguous operands
+  using LA = TileLayout<T, BM, BK, AK>;
+  using LB = TileLayout<T, BN, BK, BKC>;
+  constexpr int kTileBytes = 2 * (LA::kElems + LB::kElems) * sizeof(T);
+  constexpr int kOutBytes = WTM * (BN + 4) * 4;
+  __shared__ __attribute__((aligned(16)))
+  unsigned char lds_raw[kTileBytes > kOutBytes ? kTileBytes : kOutBytes];
+  T* const base = reinterpret_cast<T*>(lds_raw);
+  auto lds_a = [&](int s) { return base + s * LA::kElems; };
+  auto lds_b = [&](int s) { return base + 2 * LA::kElems + s * LB::kElems; };
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int nwg = g.tiles_m * g.tiles_n;
+  int bid = blockIdx.x;
+  if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+  const int group_span = kGroupM * g.tiles_n;
+  const int first_m = (bid / group_span) * kGroupM;
+  const int gsz = min(g.tiles_m - first_m, kGroupM);
+  const int tm = first_m + (bid % group_span) % gsz;
+  const int tn = (bid % group_span) / gsz;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const long long batch = blockIdx.y;
+
+  BufferLoader<T, BM, BK, NT, AK> la;
+  BufferLoader<T, BN, BK, NT, BKC> lb;
+  la.init(static_cast<const T*>(g.a) + batch * g.bsa,
+          static_cast<long long>(AK ? g.m : g.k) * g.lda * sizeof(T), g.lda,
+          tid);
+  lb.init(static_cast<const T*>(g.b) + batch * g.bsb,
+          static_cast<long long>(BKC ? g.n : g.k) * g.ldb * sizeof(T), g.ldb,
+          tid);
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int ktiles = g.k / BK;  // >= 1
+  la.load(m0, 0);
+  lb.load(n0, 0);
+  la.store(lds_a(0), tid);
+  lb.store(lds_b(0), tid);
+  __syncthreads();
+  typename Frag<T>::type fa[2][FM], fb[2][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+    fa[0][i] = load_frag<T, BM, BK, AK>(lds_a(0), wm * WTM + i * 32, 0, lane);
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+    fb[0][j] = load_frag<T, BN, BK, BKC>(lds_b(0), wn * WTN + j * 32, 0, lane);
+  {
+    const int k1 = min(1, ktiles - 1) * BK;
+    la.load(m0, k1);
+    lb.load(n0, k1);
+  }
+  // DS reads per K step (a transposing fragment read is two instructions).
+  constexpr int kReads = FM * (AK ? 1 : 2) + FN * (BKC ? 1 : 2);
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int cur = kt & 1;
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int fc = s & 1, fn = fc ^ 1;
+      if (s + 1 < BK / 16) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          fa[fn][i] = load_frag<T, BM, BK, AK>(lds_a(cur), wm * WTM + i * 32,
+                                               (s + 1) * 16, lane);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          fb[fn][j] = load_frag<T, BN, BK, BKC>(lds_b(cur), wn * WTN + j * 32,
+                                                (s + 1) * 16, lane);
+      }
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int row = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            const int col = wn * WTN + j * 32 + (lane & 31);
-            stage[row * kLdo + col] = acc[i][j][r];
-          }
-    }
-    __syncthreads();
-#pragma unroll 1
-    for (int q = tid; q < kSlab * BN / 4; q += NT) {
-      const int lr = q / (BN / 4), lc = (q % (BN / 4)) * 4;
-      const int row = m0 + slab * WTM + lr, col = n0 + lc;
-      if (row >= g.m || col >= g.n) continue;
-      const float4 a4 = *reinterpret_cast<const float4*>(stage + lr * kLdo + lc);
-      float v[4] = {a4.x, a4.y, a4.z, a4.w};
-      const long long idx = dbase + static_cast<long long>(row) * g.ldd + col;
-      const int cnt = min(4, g.n - col);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (e >= cnt) break;
-        float x = g.alpha * v[e];
-        if (g.use_c) x += g.beta * ld_out<T>(g.c, idx + e, of32);
-        if (g.has_bias) x += ld_out<T>(g.bias, col + e, of32);
-        if (g.has_aux) st_out<T>(g.aux, idx + e, of32, x);
-        v[e] = act_f32(g.act, x);
+        for (int j = 0; j < FN; ++j) mma(acc[i][j], fa[fc][i], fb[fc][j]);
+      if (s + 1 == BK / 16) {
+        // Nobody reads the other stage during this tile: its last reader
+        // was the previous tile, which ended on a barrier.
+        la.store(lds_a(cur ^ 1), tid);
+        lb.store(lds_b(cur ^ 1), tid);
       }
-      if (vec_out && cnt == 4) {
-        if (of32) {
-          *reinterpret_cast<float4*>(static_cast<float*>(g.d) + idx) =
-              make_float4(v[0], v[1], v[2], v[3]);
-        } else {
-          union {
-            u32x2 u;
-            T e[4];
-          } o;
+      // One MFMA, then one DS read (steps 0..2) or one DS write (step 3).
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o.e[e] = from_f32<T>(v[e]);
-          *reinterpret_cast<u32x2*>(static_cast<T*>(g.d) + idx) = o.u;
-        }
-      } else {
-        for (int e = 0; e < cnt; ++e) st_out<T>(g.d, idx + e, of32, v[e]);
+      for (int q = 0; q < FM * FN; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (s + 1 < BK / 16 && q < kReads)
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (s + 1 == BK / 16 && q < la.NV + lb.NV)
+          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
       }
     }
     __syncthreads();
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      fa[0][i] = load_frag<T, BM, BK, AK>(lds_a(cur ^ 1), wm * WTM + i * 32, 0,
+                                          lane);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      fb[0][j] = load_frag<T, BN, BK, BKC>(lds_b(cur ^ 1), wn * WTN + j * 32,
+                                           0, lane);
+    // The tile after next (clamped: the last tiles reload the final one).
+    const int k2 = min(kt + 2, ktiles - 1) * BK;
+    la.load(m0, k2);
+    lb.load(n0, k2);
   }
+  // The fragment reads after the last barrier touch the stage the epilogue
+  // overwrites first.
+  __syncthreads();
+  store_tile<T, BM, BN, WM, WN>(g, acc, lds_raw, m0, n0, batch, tid);
 }
 
 

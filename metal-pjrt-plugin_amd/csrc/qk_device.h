@@ -59,16 +59,26 @@ __device__ __forceinline__ void store_any(void* p, int64_t i, int dtype,
     static_cast<float*>(p)[i] = v;
 }
 
+// 1 / (1 + e^-t) from the hardware base-2 exponential and reciprocal
+// (each within 1 ulp): t = -inf gives 0, t = +inf gives 1, NaN stays NaN.
+__device__ __forceinline__ float sigmoid_f32(float t) {
+  const float e = __builtin_amdgcn_exp2f(t * -1.4426950408889634f);  // e^-t
+  return __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 // cuBLASLt epilogue activations, in f32 (the reference's steel_act,
 // metal_pjrt/kernels/steel_gemm.metal:57-66): ReLU keeps NaN, GELU is the
-// tanh form, SiLU is x / (1 + exp(-x)).
+// tanh form, SiLU is x / (1 + exp(-x)). Both smooth activations are
+// evaluated as x * sigmoid(.): 0.5 (1 + tanh(u)) = 1 / (1 + e^-2u), so
+// GELU(x) = x * sigmoid(2u) with u = sqrt(2/pi) (x + 0.044715 x^3). The
+// infinities give what the quotient forms give (+inf -> +inf, -inf -> NaN).
 __device__ __forceinline__ float act_f32(int act, float x) {
   if (act == 1) return x != x ? x : (x > 0.0f ? x : 0.0f);
   if (act == 2) {
-    const float k = 0.7978845608028654f;  // sqrt(2/pi)
-    return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
+    const float k2 = 2.0f * 0.7978845608028654f;  // 2 sqrt(2/pi)
+    return x * sigmoid_f32(k2 * (x + 0.044715f * x * x * x));
   }
-  if (act == 3) return x / (1.0f + expf(-x));
+  if (act == 3) return x * sigmoid_f32(x);
   return x;
 }
 

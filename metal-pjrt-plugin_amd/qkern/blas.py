@@ -132,11 +132,12 @@ class MatmulPlan:
 
     def __init__(self, handle):
         self._h = handle
+        self._destroy = lib().qk_gemm_plan_destroy  # outlives module teardown
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h and _lib._lib is not None:
-            _lib._lib.qk_gemm_plan_destroy(h)
+        if h:
+            self._destroy(h)
             self._h = None
 
     def describe(self):

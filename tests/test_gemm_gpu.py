@@ -177,6 +177,72 @@ def test_all_tile_configs(dev, shape, kernel):
     assert "128x128" in plan.describe()
 
 
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_interior_tile_kernel(dev, ta, tb):
+    """Tile-multiple shapes run the unchecked interior-tile kernel."""
+    plan = run_case(dev, 2048, 2048, 128, ta=ta, tb=tb)
+    assert "gemm_fast_bf16_256x128" in plan.describe()
+    plan = run_case(dev, 4096, 4096, 64, ta=ta, tb=tb, beta=1.0,
+                    tin="float16")
+    assert "gemm_fast_f16_256x256" in plan.describe()
+
+
+def test_interior_tile_kernel_epilogues(dev):
+    plan = run_case(dev, 2048, 2048, 192, tin="float16",
+                    epilogue=Epilogue.kBiasThenSILUWithAux, separate_c=True,
+                    beta=0.5)
+    assert "gemm_fast" in plan.describe()
+    plan = run_case(dev, 2048, 2048, 64, tout="float32", tb=True,
+                    epilogue=Epilogue.kBiasThenGELU, alpha=0.5)
+    assert "gemm_fast" in plan.describe()
+    # batched with 8-element row padding (still 16-byte aligned rows)
+    plan = run_case(dev, 1024, 2048, 128, batch=4, pad=8, beta=1.0)
+    assert "gemm_fast" in plan.describe()
+
+
+def test_interior_tile_kernel_not_taken(dev):
+    # rows not 16-byte aligned, K not a multiple of 64, M not of 256
+    for kw in (dict(m=2048, n=2048, k=128, pad=3), dict(m=2048, n=2048, k=96),
+               dict(m=2000, n=2048, k=128)):
+        kw = dict(kw)
+        plan = run_case(dev, kw.pop("m"), kw.pop("n"), kw.pop("k"), **kw)
+        assert "gemm_tile" in plan.describe()
+
+
+@pytest.mark.parametrize("epilogue", [Epilogue.kReLU, Epilogue.kGELU,
+                                      Epilogue.kSILU])
+def test_activation_special_values(dev, epilogue):
+    """K = 1 and A = 1, so the pre-activation is exactly B: the activation
+    over zeros, signed zeros, saturating magnitudes, infinities and NaN, in
+    f32 within 1e-5 (NaN where the quotient forms give NaN)."""
+    vals = np.array([0.0, -0.0, 1e-30, -1e-30, 0.5, -0.5, 1.0, -1.0, 3.0,
+                     -3.0, 20.0, -20.0, 88.0, -88.0, 100.0, -100.0, 1e20,
+                     -1e20, np.inf, -np.inf, np.nan, 1e-3, -1e-3, 7.25],
+                    dtype=np.float32)
+    n = vals.size
+    m = 3
+    a = torch.ones(m, 1, dtype=torch.float32, device=dev)
+    b = torch.from_numpy(vals.reshape(1, n)).to(dev)
+    lay = lambda r, c: MatrixLayout("float32", r, c)
+    plan = BlasLt.get_matmul_plan(
+        GemmConfig(lay(m, 1), lay(1, n), lay(m, n), lay(m, n)), epilogue)
+    d = torch.empty(m, n, dtype=torch.float32, device=dev)
+    plan.execute_on_stream(None, MemoryArgs(a, b, None, d))
+    torch.cuda.synchronize()
+    _, act, _ = O.EPILOGUES[int(epilogue)]
+    with np.errstate(all="ignore"):
+        want = O.ACTS[act](vals.astype(np.float64))
+    got = d.cpu().numpy().astype(np.float64)
+    for row in got:
+        same_nan = np.isnan(row) == np.isnan(want)
+        assert same_nan.all(), (vals[~same_nan], row[~same_nan])
+        with np.errstate(invalid="ignore"):
+            ok = np.isnan(want) | (row == want) | \
+                (np.abs(row - want) <= 1e-5 * (np.abs(want) + 1e-30))
+        assert ok.all(), list(zip(vals[~ok], row[~ok], want[~ok]))
+
+
 def test_large_k(dev):
     run_case(dev, 64, 64, 4096, tout="float32")
     run_case(dev, 64, 64, 4096, tin="float32")
