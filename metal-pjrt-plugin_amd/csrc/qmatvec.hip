@@ -23,6 +23,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+
 #include <algorithm>
 #include <cstdint>
 #include <string>
@@ -555,12 +557,15 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_stream_kernel(
 }
 
 // The decode hot path: M = 1, bf16 x, 4-bit codes, group size 64, bf16
-// scales/offsets, rows whose 16-byte chunks split evenly over the 64 lanes
-// in pairs. Lane l owns the groups l, l + 64, ... (two chunks each), so it
-// loads one scale and one offset per group and a wave's loads stay
-// contiguous across lanes. x is held in registers
-// (a lane's chunks are the same for every row); codes become (128 + q)
-// bf16 pairs with one v_and_or_b32 each; rows are reduced with DPP.
+// scales/offsets, rows of 128 k-chunks of 16 bytes (k a multiple of 4096
+// for 4-bit codes). Lane l reads chunk 64 j + l for j < CPL, so every
+// wave-wide load is 1 KB of contiguous codes. The two lanes of a pair hold
+// the two halves of the same groups; one DPP swap hands each lane both
+// halves of one group per chunk pair (the even lane the group of the even
+// chunk, the odd lane the group of the odd one), so each lane loads one
+// scale and one offset per chunk pair. x is held in registers (a lane's
+// chunks are the same for every row); codes become (128 + q) bf16 pairs
+// with one v_and_or_b32 each; rows are reduced with DPP.
 template <int PACK, int CPL>
 __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -569,30 +574,52 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
   u32x4* xq = reinterpret_cast<u32x4*>(smem);
   float* xs_lds = reinterpret_cast<float*>(smem + 4 * cpr * 16);
   const int lane = threadIdx.x & 63;
-  const int gw = blockIdx.x * (kStreamThreads / 64) + (threadIdx.x >> 6);
+  const int odd = lane & 1;
+  // Row indices are wave-uniform: keep them in SGPRs, so a row's loads
+  // differ only in their scalar offset.
+  const int gw = __builtin_amdgcn_readfirstlane(
+      blockIdx.x * (kStreamThreads / 64) + (threadIdx.x >> 6));
   const int GW = gridDim.x * (kStreamThreads / 64);
   constexpr int D = CPL <= 2 ? 4 : (CPL <= 4 ? 3 : 2);
   constexpr int groups = cpr / 2;
+  // Group of chunk 64 j + l is 32 j + l/2; after the swap the lane keeps,
+  // for chunk pair t, group 64 t + 32 odd + l/2.
+  const int goff = 32 * odd + (lane >> 1);
 
-  const uint8_t* cbase = a.codes + lane * 32;
-  const bf16* S = static_cast<const bf16*>(a.scales) + lane;
-  const bf16* Bo = static_cast<const bf16*>(a.biases) + lane;
+  // Buffer descriptors (the launcher keeps every extent under 2^31 bytes);
+  // per-lane byte offsets are constants, the row offset is scalar.
+  const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(a.codes), (short)0, a.n * a.row_bytes, 0x00020000);
+  const int sb_bytes = a.n * groups * 2;
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(a.scales), (short)0, sb_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(a.biases), (short)0, a.has_bias ? sb_bytes : 0,
+      0x00020000);
+  const int cvoff = lane * 16, svoff = goff * 2;
+  constexpr int kNonTemporal = 2;  // nt: streamed once
 
   struct Slot {
     u32x4 w[CPL];
     float s[G], b[G];
   };
   auto load_row = [&](int row, Slot& r) {
-    const uint8_t* p = cbase + static_cast<long long>(row) * a.row_bytes;
+    const int co = row * a.row_bytes, so = row * groups * 2;
 #pragma unroll
-    for (int j = 0; j < CPL; ++j)  // chunk j: group j/2, half j%2
-      r.w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-          p + 2048 * (j >> 1) + 16 * (j & 1)));
-    const long long gb = static_cast<long long>(row) * groups;
+    for (int j = 0; j < CPL; ++j)
+      r.w[j] = __builtin_amdgcn_raw_buffer_load_b128(crs, cvoff + 1024 * j, co,
+                                                     kNonTemporal);
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      r.s[h] = to_f32(S[gb + 64 * h]);
-      r.b[h] = a.has_bias ? to_f32(Bo[gb + 64 * h]) : 0.f;
+    for (int t = 0; t < G; ++t) {
+      r.s[t] = __uint_as_float(static_cast<uint32_t>(
+                   __builtin_amdgcn_raw_buffer_load_b16(srs, svoff + 128 * t,
+                                                        so, 0))
+                               << 16);
+      // A descriptor of extent 0 reads zeros when there are no offsets.
+      r.b[t] = __uint_as_float(static_cast<uint32_t>(
+                   __builtin_amdgcn_raw_buffer_load_b16(brs, svoff + 128 * t,
+                                                        so, 0))
+                               << 16);
     }
   };
 
@@ -608,14 +635,13 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
   float xsum[G];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const int c = 2 * (lane + 64 * (j >> 1)) + (j & 1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xr[j][i] = xq[i * cpr + c];
+    for (int i = 0; i < 4; ++i) xr[j][i] = xq[i * cpr + 64 * j + lane];
   }
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const int c = 2 * (lane + 64 * h);
-    xsum[h] = xs_lds[c] + xs_lds[c + 1];
+  for (int t = 0; t < G; ++t) {
+    const int g = 64 * t + goff;
+    xsum[t] = xs_lds[2 * g] + xs_lds[2 * g + 1];
   }
   const uint32_t kMask = vgpr_const(0x000F000Fu);
   const uint32_t kBias = vgpr_const(0x43004300u);
@@ -623,11 +649,11 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
   auto compute_row = [&](int row, const Slot& r) {
     float acc = 0.f;
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float d = 0.f;
+    for (int t = 0; t < G; ++t) {
+      float d[2] = {0.f, 0.f};
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        const int j = 2 * h + jj;
+        const int j = 2 * t + jj;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t word = r.w[j][i];
@@ -635,12 +661,16 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
           for (int sh = 0; sh < 4; ++sh) {
             const uint32_t cp = ((word >> (4 * sh)) & kMask) | kBias;
             const uint32_t xp = xr[j][i][sh];
-            d = __builtin_amdgcn_fdot2_f32_bf16(AsBf16x2(cp), AsBf16x2(xp), d,
-                                                false);
+            d[jj] = __builtin_amdgcn_fdot2_f32_bf16(
+                AsBf16x2(cp), AsBf16x2(xp), d[jj], false);
           }
         }
       }
-      acc = fmaf(r.s[h], d, fmaf(r.b[h] - 128.f * r.s[h], xsum[h], acc));
+      // Keep the half of the own group, pass the partner its half.
+      const float keep = odd ? d[1] : d[0];
+      const float give = odd ? d[0] : d[1];
+      const float dg = keep + dpp_f32<0xB1>(give);  // swap within lane pairs
+      acc = fmaf(r.s[t], dg, fmaf(r.b[t] - 128.f * r.s[t], xsum[t], acc));
     }
     const float v = wave_sum_dpp(acc);
     if (lane == 0) static_cast<bf16*>(a.y)[row] = from_f32<bf16>(v);
@@ -658,16 +688,31 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
   }
 }
 
+// QK_QMV_WG_PER_CU=<n> caps the resident workgroups per CU of the
+// streaming kernels (tuning only).
+int QmvWgPerCuCap() {
+  static const int cap = [] {
+    const char* v = std::getenv("QK_QMV_WG_PER_CU");
+    if (v == nullptr || *v < '1' || *v > '9') return 1 << 30;
+    return std::atoi(v);
+  }();
+  return cap;
+}
+
 template <int PACK>
 bool LaunchM1(const QmvArgs& a, int cus, hipStream_t stream, qk_status* st) {
   const int cpr = a.row_bytes / 16;
   if (a.m != 1 || a.group != 64 || cpr % 128 != 0) return false;
+  // Buffer descriptors cover at most 2^31 bytes of codes.
+  if (static_cast<int64_t>(a.n) * a.row_bytes >= (int64_t{1} << 31))
+    return false;
   const int cpl = cpr / 64;
   const size_t lds = static_cast<size_t>(cpr) * (64 + 4);
   const int need = (a.n + 3) / 4;
   auto go = [&](auto kernel) {
-    const int per_cu = ResidentBlocks(reinterpret_cast<const void*>(kernel),
-                                      kStreamThreads, lds);
+    const int per_cu = std::min(QmvWgPerCuCap(),
+        ResidentBlocks(reinterpret_cast<const void*>(kernel), kStreamThreads,
+                       lds));
     const int grid = std::max(1, std::min(need, cus * per_cu));
     kernel<<<grid, kStreamThreads, lds, stream>>>(a);
     *st = PostLaunch("qmv_m1");
@@ -696,8 +741,9 @@ qk_status LaunchStreamMT(QmvArgs a, int cpl, int cus, hipStream_t st) {
   // As many workgroups as the GPU keeps resident (each wave then walks
   // its rows with a prefetch), at most one row per wave.
   auto go = [&](auto kernel) {
-    const int per_cu = ResidentBlocks(reinterpret_cast<const void*>(kernel),
-                                      kStreamThreads, lds);
+    const int per_cu = std::min(QmvWgPerCuCap(),
+        ResidentBlocks(reinterpret_cast<const void*>(kernel), kStreamThreads,
+                       lds));
     const int grid = std::max(1, std::min(need, cus * per_cu));
     kernel<<<grid, kStreamThreads, lds, st>>>(a);
     return PostLaunch("qmv_stream");

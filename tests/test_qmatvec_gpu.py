@@ -89,6 +89,34 @@ def test_qmatvec_small(dev, packing, xdt):
         check_matvec(y.float().cpu().numpy().astype(np.float64), x, w)
 
 
+@pytest.mark.parametrize("packing", [Packing.U32X8, Packing.BYTE_HALFSPLIT])
+@pytest.mark.parametrize("k", [4096, 8192, 12288, 16384])
+def test_qmatvec_single_row_paths(dev, packing, k):
+    """M = 1, bf16 x, group 64: the decode kernel (x loaded per lane), for
+    every chunks-per-lane count, ragged N, with and without offsets; an x
+    that is not 16-byte aligned is rejected."""
+    rng = np.random.default_rng(k + int(packing))
+    for n, has_bias in ((300, True), (77, False)):
+        dc, ds, db, w, *_ = make_weights(rng, n, k, packing, 64,
+                                         has_bias=has_bias)
+        x = O.round_to(rng.standard_normal((1, k)), "bfloat16").astype(
+            np.float32)
+        base = torch.zeros(k + 8, dtype=torch.bfloat16, device=dev)
+        for off in (0, 1):
+            dx = base[off:off + k].view(1, k)
+            dx.copy_(torch.from_numpy(x).to(torch.bfloat16))
+            call = lambda: qkern.qmatvec(dx, dc.to(dev), ds.to(dev),
+                                         None if db is None else db.to(dev),
+                                         packing=packing, group_size=64)
+            if off:
+                with pytest.raises(qkern.QkError, match="16-byte aligned"):
+                    call()
+                continue
+            y = call()
+            torch.cuda.synchronize()
+            check_matvec(y.float().cpu().numpy().astype(np.float64), x, w)
+
+
 def test_qmatvec_leading_dims_and_no_bias(dev):
     rng = np.random.default_rng(5)
     dc, ds, _, w, *_ = make_weights(rng, 40, 256, Packing.U32X8, 64,
