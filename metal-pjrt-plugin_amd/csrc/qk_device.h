@@ -113,6 +113,24 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// Sums of four values over the 64 lanes of a wavefront at once: lane l
+// returns the total of value (l & 3). Two quad-transpose steps leave each
+// lane with the quad sum of one value, two DPP rotations within rows of
+// 16 and two cross-row swaps finish the sum: 10 cross-lane operations in
+// all instead of 4 x 8.
+__device__ __forceinline__ float wave_sum4(float a0, float a1, float a2,
+                                           float a3, int lane) {
+  const bool b0 = lane & 1, b1 = lane & 2;
+  const float v01 = (b0 ? a1 : a0) + dpp_f32<0xB1>(b0 ? a0 : a1);
+  const float v23 = (b0 ? a3 : a2) + dpp_f32<0xB1>(b0 ? a2 : a3);
+  float v = (b1 ? v23 : v01) + dpp_f32<0x4E>(b1 ? v01 : v23);
+  v += dpp_f32<0x124>(v);  // row_ror:4
+  v += dpp_f32<0x128>(v);  // row_ror:8
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 // Sum / max over the 64 lanes of a wavefront; every lane gets the result.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

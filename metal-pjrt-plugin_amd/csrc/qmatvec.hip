@@ -646,7 +646,8 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
   const uint32_t kMask = vgpr_const(0x000F000Fu);
   const uint32_t kBias = vgpr_const(0x43004300u);
 
-  auto compute_row = [&](int row, const Slot& r) {
+  // Partial dot product of this lane's chunks with one row.
+  auto row_acc = [&](const Slot& r) {
     float acc = 0.f;
 #pragma unroll
     for (int t = 0; t < G; ++t) {
@@ -672,18 +673,29 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
       const float dg = keep + dpp_f32<0xB1>(give);  // swap within lane pairs
       acc = fmaf(r.s[t], dg, fmaf(r.b[t] - 128.f * r.s[t], xsum[t], acc));
     }
-    const float v = wave_sum_dpp(acc);
-    if (lane == 0) static_cast<bf16*>(a.y)[row] = from_f32<bf16>(v);
+    return acc;
   };
 
+  bf16* Y = static_cast<bf16*>(a.y);
   for (int row = gw; row < a.n; row += D * GW) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int r = row + d * GW;
-      if (r >= a.n) break;
-      compute_row(r, buf[d]);
-      const int nr = r + D * GW;
-      if (nr < a.n) load_row(nr, buf[d]);
+      if (r < a.n) {
+        acc[d] = row_acc(buf[d]);
+        const int nr = r + D * GW;
+        if (nr < a.n) load_row(nr, buf[d]);
+      }
+    }
+    if (row + GW >= a.n) {  // one row this round (small matrices)
+      const float v = wave_sum_dpp(acc[0]);
+      if (lane == 0) Y[row] = from_f32<bf16>(v);
+    } else {
+      // Lanes 0..D-1 get the totals of rows row + lane * GW.
+      const float v = wave_sum4(acc[0], acc[1], acc[2], acc[3], lane);
+      const int rr = row + (lane & 3) * GW;
+      if (lane < D && rr < a.n) Y[rr] = from_f32<bf16>(v);
     }
   }
 }
