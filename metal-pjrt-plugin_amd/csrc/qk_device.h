@@ -91,6 +91,15 @@ __device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
   return r;
 }
 
+// 64-bit logical right shift by a constant as one v_lshrrev_b64 (the
+// compiler would otherwise split it into a funnel shift and a shift).
+template <int kS>
+__device__ __forceinline__ uint64_t shr64(uint64_t v) {
+  uint64_t r;
+  asm("v_lshrrev_b64 %0, %1, %2" : "=v"(r) : "i"(kS), "v"(v));
+  return r;
+}
+
 // Sum over the 64 lanes of a wavefront with DPP row operations (quad
 // swaps, half-row and row mirrors) and four lane reads; the result is
 // wave-uniform.

@@ -656,14 +656,23 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
       for (int jj = 0; jj < 2; ++jj) {
         const int j = 2 * t + jj;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t word = r.w[j][i];
+        for (int p = 0; p < 2; ++p) {
+          // Words 2p and 2p+1 shifted together: the bits the low word
+          // takes from the high one land above bit 19, outside kMask.
+          const uint64_t v = (static_cast<uint64_t>(r.w[j][2 * p + 1]) << 32) |
+                             r.w[j][2 * p];
+          const uint64_t sv[4] = {v, shr64<4>(v), shr64<8>(v), shr64<12>(v)};
 #pragma unroll
-          for (int sh = 0; sh < 4; ++sh) {
-            const uint32_t cp = ((word >> (4 * sh)) & kMask) | kBias;
-            const uint32_t xp = xr[j][i][sh];
-            d[jj] = __builtin_amdgcn_fdot2_f32_bf16(
-                AsBf16x2(cp), AsBf16x2(xp), d[jj], false);
+          for (int h = 0; h < 2; ++h) {
+            const int i = 2 * p + h;
+#pragma unroll
+            for (int sh = 0; sh < 4; ++sh) {
+              const uint32_t word = static_cast<uint32_t>(sv[sh] >> (32 * h));
+              const uint32_t cp = (word & kMask) | kBias;
+              const uint32_t xp = xr[j][i][sh];
+              d[jj] = __builtin_amdgcn_fdot2_f32_bf16(
+                  AsBf16x2(cp), AsBf16x2(xp), d[jj], false);
+            }
           }
         }
       }
