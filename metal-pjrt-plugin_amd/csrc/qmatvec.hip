@@ -362,6 +362,8 @@ __global__ void dequant_kernel(QmvArgs a, long long total_chunks) {
 // consecutive quads (no bank conflicts).
 
 constexpr int kStreamThreads = 256;
+// s_waitcnt operand: vmcnt(0), expcnt and lgkmcnt left at their maxima.
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 template <int PACK>
 struct ChunkTraits {
@@ -599,9 +601,11 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
   const int cvoff = lane * 16, svoff = goff * 2;
   constexpr int kNonTemporal = 2;  // nt: streamed once
 
+  // Scales and offsets stay raw bf16 bits until used: converting them at
+  // load time would make the prefetch wait for its own loads.
   struct Slot {
     u32x4 w[CPL];
-    float s[G], b[G];
+    uint16_t s[G], b[G];
   };
   auto load_row = [&](int row, Slot& r) {
     const int co = row * a.row_bytes, so = row * groups * 2;
@@ -611,15 +615,9 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
                                                      kNonTemporal);
 #pragma unroll
     for (int t = 0; t < G; ++t) {
-      r.s[t] = __uint_as_float(static_cast<uint32_t>(
-                   __builtin_amdgcn_raw_buffer_load_b16(srs, svoff + 128 * t,
-                                                        so, 0))
-                               << 16);
+      r.s[t] = __builtin_amdgcn_raw_buffer_load_b16(srs, svoff + 128 * t, so, 0);
       // A descriptor of extent 0 reads zeros when there are no offsets.
-      r.b[t] = __uint_as_float(static_cast<uint32_t>(
-                   __builtin_amdgcn_raw_buffer_load_b16(brs, svoff + 128 * t,
-                                                        so, 0))
-                               << 16);
+      r.b[t] = __builtin_amdgcn_raw_buffer_load_b16(brs, svoff + 128 * t, so, 0);
     }
   };
 
@@ -630,6 +628,11 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
     if (r < a.n) load_row(r, buf[d]);  // in flight while x is staged
   }
   StageX<PACK, bf16>(a, 1, cpr, xq, xs_lds);
+  // Every wave waits for its first slots here. The loop below then starts
+  // from "nothing outstanding", so its waits follow the loop body's own
+  // load order; without this, merging the prologue's order makes them
+  // wait for whole rounds of prefetch.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
   u32x4 xr[CPL][4];
   float xsum[G];
@@ -680,13 +683,29 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
       const float keep = odd ? d[1] : d[0];
       const float give = odd ? d[0] : d[1];
       const float dg = keep + dpp_f32<0xB1>(give);  // swap within lane pairs
-      acc = fmaf(r.s[t], dg, fmaf(r.b[t] - 128.f * r.s[t], xsum[t], acc));
+      const float sc = __uint_as_float(static_cast<uint32_t>(r.s[t]) << 16);
+      const float of = __uint_as_float(static_cast<uint32_t>(r.b[t]) << 16);
+      acc = fmaf(sc, dg, fmaf(of - 128.f * sc, xsum[t], acc));
     }
     return acc;
   };
 
   bf16* Y = static_cast<bf16*>(a.y);
-  for (int row = gw; row < a.n; row += D * GW) {
+  int row = gw;
+  // Steady state: this round's rows and the next round's are all in
+  // range, so the prefetch is unconditional (no merge of old and new
+  // slot contents that would wait on the loads just issued).
+  for (; row + (2 * D - 1) * GW < a.n; row += D * GW) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      acc[d] = row_acc(buf[d]);
+      load_row(row + (d + D) * GW, buf[d]);
+    }
+    const float v = wave_sum4(acc[0], acc[1], acc[2], acc[3], lane);
+    if (lane < D) Y[row + lane * GW] = from_f32<bf16>(v);
+  }
+  for (; row < a.n; row += D * GW) {
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < D; ++d) {
