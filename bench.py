@@ -296,17 +296,21 @@ def main():
     # achieved: algorithmic bytes per launch / device time per launch, over
     # the same timed region (4 launches per step)
     achieved = step_bytes * args.steps / (gpu_ms * 1e-3) / 1e9
-    # per-shape breakdown: 30 back-to-back launches of one shape (rotating
-    # weight sets) between two events
+    del warm, timed, sets
+    # per-shape breakdown: 30 back-to-back launches of one shape between two
+    # events, rotating over at least 512 MB of weight copies so that no
+    # launch finds its weights in the 256 MB last-level cache
     shapes = []
     for j, (n, k) in enumerate(QWEN3_8B):
+        copies = max(2, -(-(512 << 20) // per_shape_bytes[j]))
+        wset = [make_int4(torch, dev, n, k, gen) for _ in range(copies)]
         ms = timed_launches(
-            torch, lambda i: qkern.qmatvec(xs[j], *sets[i % rot][j],
+            torch, lambda i: qkern.qmatvec(xs[j], *wset[i % copies],
                                            out=ys[j]), 30)
         shapes.append({"n": n, "k": k, "us": round(ms * 1e3, 2),
                        "gbs": round(per_shape_bytes[j] / (ms * 1e-3) / 1e9,
                                     1)})
-    del warm, timed, sets
+        del wset
 
     result = {
         "metric": "int4 GEMV HBM GB/s (% of peak); bf16 GEMM TFLOP/s "

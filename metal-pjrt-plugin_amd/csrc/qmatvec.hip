@@ -558,6 +558,66 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_stream_kernel(
   }
 }
 
+// x of one 4-bit chunk (group size 64) in registers, as loaded: the 32
+// elements of a u32x8 chunk (64 contiguous bytes), or the two 16-element
+// runs [kb, kb + 16) and [kb + 32, kb + 48) of a half-split chunk, with
+// kb = 64 (c / 2) + 16 (c % 2).
+template <int PACK>
+__device__ __forceinline__ void LoadXChunk(const bf16* X, int c,
+                                           u32x4 (&v)[4]) {
+  if constexpr (PACK == QK_PACK_U32X8) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(X + 32 * c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = src[i];
+  } else {
+    const bf16* base = X + 64 * (c >> 1) + 16 * (c & 1);
+    const u32x4* lo = reinterpret_cast<const u32x4*>(base);
+    const u32x4* hi = reinterpret_cast<const u32x4*>(base + 32);
+    v[0] = lo[0], v[1] = lo[1], v[2] = hi[0], v[3] = hi[1];
+  }
+}
+
+// The loaded chunk as the bf16 pairs that meet the code pairs (nibbles
+// sh, sh + 4) of each code word: xp[i][sh] = (x[e(i, sh)], x[e(i, sh+4)]),
+// e as in Int4Elem, one byte permute per pair; returns the chunk's sum.
+template <int PACK>
+__device__ __forceinline__ float XChunkPairs(const u32x4 (&v)[4],
+                                             u32x4 (&xp)[4]) {
+  constexpr uint32_t kLoLo = 0x05040100u, kHiHi = 0x07060302u;
+  if constexpr (PACK == QK_PACK_U32X8) {
+    // v[i] holds x[8i .. 8i + 8) as pairs (x0,x1) (x2,x3) (x4,x5) (x6,x7)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      xp[i][0] = __builtin_amdgcn_perm(v[i][2], v[i][0], kLoLo);  // x0, x4
+      xp[i][1] = __builtin_amdgcn_perm(v[i][2], v[i][0], kHiHi);  // x1, x5
+      xp[i][2] = __builtin_amdgcn_perm(v[i][3], v[i][1], kLoLo);  // x2, x6
+      xp[i][3] = __builtin_amdgcn_perm(v[i][3], v[i][1], kHiHi);  // x3, x7
+    }
+  } else {
+    // word i: low nibbles are elements 4i + sh/2 of the low run (even sh)
+    // or of the high run (odd sh), high nibbles the same plus 2.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4& L = v[i >> 1];
+      const u32x4& H = v[2 + (i >> 1)];
+      const int w = 2 * (i & 1);
+      xp[i][0] = __builtin_amdgcn_perm(L[w + 1], L[w], kLoLo);
+      xp[i][1] = __builtin_amdgcn_perm(H[w + 1], H[w], kLoLo);
+      xp[i][2] = __builtin_amdgcn_perm(L[w + 1], L[w], kHiHi);
+      xp[i][3] = __builtin_amdgcn_perm(H[w + 1], H[w], kHiHi);
+    }
+  }
+  const uint32_t ones = 0x3F803F80u;  // bf16 (1, 1)
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int sh = 0; sh < 4; ++sh)
+      sum = __builtin_amdgcn_fdot2_f32_bf16(AsBf16x2(xp[i][sh]),
+                                            AsBf16x2(ones), sum, false);
+  return sum;
+}
+
 // The decode hot path: M = 1, bf16 x, 4-bit codes, group size 64, bf16
 // scales/offsets, rows of 128 k-chunks of 16 bytes (k a multiple of 4096
 // for 4-bit codes). Lane l reads chunk 64 j + l for j < CPL, so every
@@ -568,7 +628,7 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_stream_kernel(
 // scale and one offset per chunk pair. x is held in registers (a lane's
 // chunks are the same for every row); codes become (128 + q) bf16 pairs
 // with one v_and_or_b32 each; rows are reduced with DPP.
-template <int PACK, int CPL>
+template <int PACK, int CPL, int D>
 __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int cpr = 64 * CPL;
@@ -582,7 +642,6 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
   const int gw = __builtin_amdgcn_readfirstlane(
       blockIdx.x * (kStreamThreads / 64) + (threadIdx.x >> 6));
   const int GW = gridDim.x * (kStreamThreads / 64);
-  constexpr int D = CPL <= 2 ? 4 : (CPL <= 4 ? 3 : 2);
   constexpr int groups = cpr / 2;
   // Group of chunk 64 j + l is 32 j + l/2; after the swap the lane keeps,
   // for chunk pair t, group 64 t + 32 odd + l/2.
@@ -607,33 +666,58 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
     u32x4 w[CPL];
     uint16_t s[G], b[G];
   };
-  auto load_row = [&](int row, Slot& r) {
-    const int co = row * a.row_bytes, so = row * groups * 2;
+  // `skip` (prologue rows past the end) moves the per-lane offsets past
+  // every descriptor's extent: such loads return zeros and touch no
+  // memory, and every wave issues the same loads (no branch).
+  auto load_row = [&](int row, Slot& r, bool skip = false) {
+    const int co = skip ? 0 : row * a.row_bytes;
+    const int so = skip ? 0 : row * groups * 2;
+    const int oob = skip ? 0x7FFF0000 : 0;
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
-      r.w[j] = __builtin_amdgcn_raw_buffer_load_b128(crs, cvoff + 1024 * j, co,
-                                                     kNonTemporal);
+      r.w[j] = __builtin_amdgcn_raw_buffer_load_b128(
+          crs, cvoff + oob + 1024 * j, co, kNonTemporal);
 #pragma unroll
     for (int t = 0; t < G; ++t) {
-      r.s[t] = __builtin_amdgcn_raw_buffer_load_b16(srs, svoff + 128 * t, so, 0);
+      r.s[t] = __builtin_amdgcn_raw_buffer_load_b16(srs, svoff + oob + 128 * t,
+                                                    so, 0);
       // A descriptor of extent 0 reads zeros when there are no offsets.
-      r.b[t] = __builtin_amdgcn_raw_buffer_load_b16(brs, svoff + 128 * t, so, 0);
+      r.b[t] = __builtin_amdgcn_raw_buffer_load_b16(brs, svoff + oob + 128 * t,
+                                                    so, 0);
     }
   };
 
+  // x is requested first: loads complete in order, so x can be staged
+  // while the rows requested after it are still in flight.
+  constexpr int XPT = (cpr + kStreamThreads - 1) / kStreamThreads;
+  u32x4 xraw[XPT][4];
+#pragma unroll
+  for (int q = 0; q < XPT; ++q) {
+    const int c = threadIdx.x + q * kStreamThreads;
+    if (c < cpr) LoadXChunk<PACK>(static_cast<const bf16*>(a.x), c, xraw[q]);
+  }
   Slot buf[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
     const int r = gw + d * GW;
-    if (r < a.n) load_row(r, buf[d]);  // in flight while x is staged
+    load_row(r, buf[d], r >= a.n);
   }
-  StageX<PACK, bf16>(a, 1, cpr, xq, xs_lds);
+#pragma unroll
+  for (int q = 0; q < XPT; ++q) {
+    const int c = threadIdx.x + q * kStreamThreads;
+    if (c < cpr) {
+      u32x4 quad[4];
+      xs_lds[c] = XChunkPairs<PACK>(xraw[q], quad);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xq[i * cpr + c] = quad[i];
+    }
+  }
   // Every wave waits for its first slots here. The loop below then starts
   // from "nothing outstanding", so its waits follow the loop body's own
   // load order; without this, merging the prologue's order makes them
   // wait for whole rounds of prefetch.
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   u32x4 xr[CPL][4];
   float xsum[G];
 #pragma unroll
@@ -695,18 +779,24 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
   // Steady state: this round's rows and the next round's are all in
   // range, so the prefetch is unconditional (no merge of old and new
   // slot contents that would wait on the loads just issued).
+  static_assert(D == 2 || D % 4 == 0, "rows are reduced four at a time");
+  constexpr int DA = D < 4 ? 4 : D;  // accumulators, padded to fours
   for (; row + (2 * D - 1) * GW < a.n; row += D * GW) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float acc[DA] = {};
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       acc[d] = row_acc(buf[d]);
       load_row(row + (d + D) * GW, buf[d]);
     }
-    const float v = wave_sum4(acc[0], acc[1], acc[2], acc[3], lane);
-    if (lane < D) Y[row + lane * GW] = from_f32<bf16>(v);
+#pragma unroll
+    for (int q = 0; q < DA; q += 4) {
+      const float v = wave_sum4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3],
+                                lane);
+      if (lane < 4 && q + lane < D) Y[row + (q + lane) * GW] = from_f32<bf16>(v);
+    }
   }
   for (; row < a.n; row += D * GW) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float acc[DA] = {};
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int r = row + d * GW;
@@ -720,23 +810,39 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
       const float v = wave_sum_dpp(acc[0]);
       if (lane == 0) Y[row] = from_f32<bf16>(v);
     } else {
-      // Lanes 0..D-1 get the totals of rows row + lane * GW.
-      const float v = wave_sum4(acc[0], acc[1], acc[2], acc[3], lane);
-      const int rr = row + (lane & 3) * GW;
-      if (lane < D && rr < a.n) Y[rr] = from_f32<bf16>(v);
+      // Lane l < 4 gets the total of row row + (q + l) * GW.
+#pragma unroll
+      for (int q = 0; q < DA; q += 4) {
+        const float v = wave_sum4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3],
+                                  lane);
+        const int rr = row + (q + (lane & 3)) * GW;
+        if (lane < 4 && q + lane < D && rr < a.n) Y[rr] = from_f32<bf16>(v);
+      }
     }
   }
 }
 
-// QK_QMV_WG_PER_CU=<n> caps the resident workgroups per CU of the
-// streaming kernels (tuning only).
-int QmvWgPerCuCap() {
-  static const int cap = [] {
+// QK_QMV_WG_PER_CU=<n> sets the workgroups per CU of the streaming
+// kernels, within what stays resident (tuning only); 0 when unset.
+int QmvWgPerCu() {
+  static const int n = [] {
     const char* v = std::getenv("QK_QMV_WG_PER_CU");
-    if (v == nullptr || *v < '1' || *v > '9') return 1 << 30;
+    if (v == nullptr || *v < '1' || *v > '9') return 0;
     return std::atoi(v);
   }();
-  return cap;
+  return n;
+}
+
+// QK_QMV_M1_DEPTH=<2|4|8> forces the rows each decode wave keeps in
+// flight (tuning only).
+int M1DepthForced() {
+  static const int d = [] {
+    const char* v = std::getenv("QK_QMV_M1_DEPTH");
+    if (v == nullptr || *v < '1' || *v > '9') return 0;
+    const int x = std::atoi(v);
+    return x == 2 || x == 4 || x == 8 ? x : 0;
+  }();
+  return d;
 }
 
 template <int PACK>
@@ -749,24 +855,38 @@ bool LaunchM1(const QmvArgs& a, int cus, hipStream_t stream, qk_status* st) {
   const int cpl = cpr / 64;
   const size_t lds = static_cast<size_t>(cpr) * (64 + 4);
   const int need = (a.n + 3) / 4;
+  // About four rows in flight per SIMD: one workgroup per CU with four
+  // rows per wave for long matrices of 4096-wide rows, else two
+  // workgroups per CU with two rows per wave. Measured on MI355X at the
+  // Qwen3-8B decode shapes, this beats full occupancy by 10-20%.
+  const bool deep = cpl == 2 && a.n >= 32768;
+  const int dflt_wg = deep ? 1 : 2, dflt_depth = deep ? 4 : 2;
   auto go = [&](auto kernel) {
-    const int per_cu = std::min(QmvWgPerCuCap(),
-        ResidentBlocks(reinterpret_cast<const void*>(kernel), kStreamThreads,
-                       lds));
+    const int resident = ResidentBlocks(reinterpret_cast<const void*>(kernel),
+                                        kStreamThreads, lds);
+    const int per_cu = std::min(QmvWgPerCu() ? QmvWgPerCu() : dflt_wg, resident);
     const int grid = std::max(1, std::min(need, cus * per_cu));
     kernel<<<grid, kStreamThreads, lds, stream>>>(a);
     *st = PostLaunch("qmv_m1");
     return true;
   };
+  auto depth = [&](auto k2, auto k4, auto k8, int dflt) {
+    const int d = M1DepthForced() ? M1DepthForced() : dflt;
+    return d == 2 ? go(k2) : d == 8 ? go(k8) : go(k4);
+  };
   switch (cpl) {
     case 2:
-      return go(qmv_m1_kernel<PACK, 2>);
+      return depth(qmv_m1_kernel<PACK, 2, 2>, qmv_m1_kernel<PACK, 2, 4>,
+                   qmv_m1_kernel<PACK, 2, 8>, dflt_depth);
     case 4:
-      return go(qmv_m1_kernel<PACK, 4>);
+      return depth(qmv_m1_kernel<PACK, 4, 2>, qmv_m1_kernel<PACK, 4, 4>,
+                   qmv_m1_kernel<PACK, 4, 8>, dflt_depth);
     case 6:
-      return go(qmv_m1_kernel<PACK, 6>);
+      return depth(qmv_m1_kernel<PACK, 6, 2>, qmv_m1_kernel<PACK, 6, 4>,
+                   qmv_m1_kernel<PACK, 6, 8>, dflt_depth);
     case 8:
-      return go(qmv_m1_kernel<PACK, 8>);
+      return depth(qmv_m1_kernel<PACK, 8, 2>, qmv_m1_kernel<PACK, 8, 4>,
+                   qmv_m1_kernel<PACK, 8, 8>, dflt_depth);
     default:
       return false;
   }
@@ -781,9 +901,10 @@ qk_status LaunchStreamMT(QmvArgs a, int cpl, int cus, hipStream_t st) {
   // As many workgroups as the GPU keeps resident (each wave then walks
   // its rows with a prefetch), at most one row per wave.
   auto go = [&](auto kernel) {
-    const int per_cu = std::min(QmvWgPerCuCap(),
-        ResidentBlocks(reinterpret_cast<const void*>(kernel), kStreamThreads,
-                       lds));
+    const int resident = ResidentBlocks(reinterpret_cast<const void*>(kernel),
+                                        kStreamThreads, lds);
+    const int per_cu = QmvWgPerCu() ? std::min(QmvWgPerCu(), resident)
+                                    : resident;
     const int grid = std::max(1, std::min(need, cus * per_cu));
     kernel<<<grid, kStreamThreads, lds, st>>>(a);
     return PostLaunch("qmv_stream");
