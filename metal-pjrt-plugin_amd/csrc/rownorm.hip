@@ -20,6 +20,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "qk_device.h"
@@ -47,10 +48,10 @@ constexpr int kThreads = 256;
 // Sum over the TPR threads that share a row (TPR = 64 or 256).
 template <int TPR>
 __device__ __forceinline__ float row_sum(float v, float* red) {
-  v = wave_sum(v);
   if constexpr (TPR == 64) {
-    return v;
+    return wave_sum_dpp(v);
   } else {
+    v = wave_sum(v);
     const int wave = threadIdx.x >> 6;
     __syncthreads();  // red may still be read by a previous reduction
     if ((threadIdx.x & 63) == 0) red[wave] = v;
@@ -152,6 +153,23 @@ __global__ __launch_bounds__(kThreads) void rownorm_kernel(RnArgs a) {
     }
   }
 
+  // Gain and offset are requested right behind x, so their latency hides
+  // under the row's own loads instead of following the reduction.
+  const bool gvec = V > 1 && (reinterpret_cast<uintptr_t>(a.gain) % 16 == 0);
+  const bool bvec = V > 1 && (reinterpret_cast<uintptr_t>(a.beta) % 16 == 0);
+  constexpr bool kParams = KIND != QK_ROWNORM_SOFTMAX;
+  float g[kParams ? VPT : 1][V], bb[KIND == QK_ROWNORM_LAYER ? VPT : 1][V];
+  if constexpr (kParams) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int base = (t + i * TPR) * V;
+      if (base >= n) continue;
+      if (a.has_gain) load_param<V>(a.gain, a.gdt, base, gvec, g[i]);
+      if (KIND == QK_ROWNORM_LAYER && a.has_beta)
+        load_param<V>(a.beta, a.bdt, base, bvec, bb[i]);
+    }
+  }
+
   float scale = 1.f, shift = 0.f;  // y = (x - shift) * scale (then gain)
   if constexpr (KIND == QK_ROWNORM_RMS) {
     float ss = 0.f;
@@ -200,8 +218,6 @@ __global__ __launch_bounds__(kThreads) void rownorm_kernel(RnArgs a) {
     scale = 1.0f / s;
   }
 
-  const bool gvec = V > 1 && (reinterpret_cast<uintptr_t>(a.gain) % 16 == 0);
-  const bool bvec = V > 1 && (reinterpret_cast<uintptr_t>(a.beta) % 16 == 0);
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int base = (t + i * TPR) * V;
@@ -209,18 +225,14 @@ __global__ __launch_bounds__(kThreads) void rownorm_kernel(RnArgs a) {
     float out[V];
 #pragma unroll
     for (int e = 0; e < V; ++e) out[e] = (v[i][e] - shift) * scale;
-    if constexpr (KIND != QK_ROWNORM_SOFTMAX) {
+    if constexpr (kParams) {
       if (a.has_gain) {
-        float g[V];
-        load_param<V>(a.gain, a.gdt, base, gvec, g);
 #pragma unroll
-        for (int e = 0; e < V; ++e) out[e] *= g[e];
+        for (int e = 0; e < V; ++e) out[e] *= g[i][e];
       }
       if (KIND == QK_ROWNORM_LAYER && a.has_beta) {
-        float bb[V];
-        load_param<V>(a.beta, a.bdt, base, bvec, bb);
 #pragma unroll
-        for (int e = 0; e < V; ++e) out[e] += bb[e];
+        for (int e = 0; e < V; ++e) out[e] += bb[KIND == QK_ROWNORM_LAYER ? i : 0][e];
       }
     }
     if constexpr (V > 1) {
@@ -231,6 +243,150 @@ __global__ __launch_bounds__(kThreads) void rownorm_kernel(RnArgs a) {
     } else {
       yr[base] = from_f32<T>(out[0]);
     }
+  }
+}
+
+// Persistent row streamer for rows that fit one wavefront's registers
+// (n <= 64 * V * VPT, 16-byte aligned rows): each wave walks rows
+// gw, gw + GW, ... with two register buffers, so the next row's loads are
+// in flight while the current row is reduced and stored; reads and writes
+// of different rows overlap instead of running as two phases. Gain and
+// offset are loaded once per wave. Every load and store goes through a
+// per-row buffer descriptor whose extent is 0 for rows past the end
+// (loads read zeros, stores are dropped), so the loop has no branches
+// and the compiler's wait counts follow the two buffers exactly.
+template <typename T, int KIND, int V, int VPT>
+__global__ __launch_bounds__(kThreads) void rownorm_stream_kernel(RnArgs a) {
+  static_assert(V > 1, "vector rows only");
+  const int lane = threadIdx.x & 63;
+  const long long gw = __builtin_amdgcn_readfirstlane(
+      blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6));
+  const long long GW = static_cast<long long>(gridDim.x) * (kThreads / 64);
+  const int n = a.n;
+  const int row_bytes = n * static_cast<int>(sizeof(T));
+  constexpr int kNT = 2;  // nontemporal: streamed once
+
+  constexpr bool kParams = KIND != QK_ROWNORM_SOFTMAX;
+  constexpr bool kBeta = KIND == QK_ROWNORM_LAYER;
+  float g[kParams ? VPT : 1][V], bb[kBeta ? VPT : 1][V];
+  if constexpr (kParams) {
+    const bool gvec = (reinterpret_cast<uintptr_t>(a.gain) % 16 == 0);
+    const bool bvec = (reinterpret_cast<uintptr_t>(a.beta) % 16 == 0);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int base = (lane + i * 64) * V;
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        g[i][e] = 1.f;
+        if (kBeta) bb[i][e] = 0.f;
+      }
+      if (base < n) {
+        if (a.has_gain) load_param<V>(a.gain, a.gdt, base, gvec, g[i]);
+        if (kBeta && a.has_beta)
+          load_param<V>(a.beta, a.bdt, base, bvec, bb[kBeta ? i : 0]);
+      }
+    }
+  }
+
+  auto rsrc = [&](const void* base, long long row) {
+    const bool ok = row < a.rows;
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(static_cast<const char*>(base)) +
+            (ok ? row : 0) * row_bytes,
+        (short)0, ok ? row_bytes : 0, 0x00020000);
+  };
+  auto load = [&](long long row, u32x4 (&buf)[VPT]) {
+    const auto rs = rsrc(a.x, row);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+      buf[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane + i * 64) * 16,
+                                                     0, kNT);
+  };
+  union Pack {
+    u32x4 u;
+    T e[V];
+  };
+  auto process = [&](long long row, const u32x4 (&buf)[VPT]) {
+    float v[VPT][V];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      Pack q;
+      q.u = buf[i];
+      const bool in = (lane + i * 64) * V < n;
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        v[i][e] = in ? to_f32(q.e[e])
+                     : (KIND == QK_ROWNORM_SOFTMAX ? -INFINITY : 0.f);
+    }
+    float scale = 1.f, shift = 0.f;
+    if constexpr (KIND == QK_ROWNORM_RMS) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+#pragma unroll
+        for (int e = 0; e < V; ++e) ss += v[i][e] * v[i][e];
+      scale = rsqrtf(wave_sum_dpp(ss) / static_cast<float>(n) + a.eps);
+    } else if constexpr (KIND == QK_ROWNORM_LAYER) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+#pragma unroll
+        for (int e = 0; e < V; ++e) s += v[i][e];
+      const float mu = wave_sum_dpp(s) / static_cast<float>(n);
+      float q = 0.f;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const bool in = (lane + i * 64) * V < n;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const float d = in ? v[i][e] - mu : 0.f;
+          q += d * d;
+        }
+      }
+      shift = mu;
+      scale = 1.0f / sqrtf(wave_sum_dpp(q) / static_cast<float>(n) + a.eps);
+    } else {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+#pragma unroll
+        for (int e = 0; e < V; ++e) mx = fmaxf(mx, v[i][e]);
+      mx = wave_max(mx);
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          v[i][e] = __expf(v[i][e] - mx);
+          s += v[i][e];
+        }
+      scale = 1.0f / wave_sum_dpp(s);
+    }
+    const auto rs = rsrc(a.y, row);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      Pack q;
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        float o = (v[i][e] - shift) * scale;
+        if constexpr (kParams) o *= g[i][e];
+        if constexpr (kBeta) o += bb[kBeta ? i : 0][e];
+        q.e[e] = from_f32<T>(o);
+      }
+      // Offsets at or past the row end are dropped by the descriptor.
+      __builtin_amdgcn_raw_buffer_store_b128(q.u, rs, (lane + i * 64) * 16, 0,
+                                             kNT);
+    }
+  };
+
+  u32x4 xa[VPT], xb[VPT];
+  load(gw, xa);
+#pragma unroll 1
+  for (long long row = gw; row < a.rows; row += 2 * GW) {
+    load(row + GW, xb);
+    process(row, xa);
+    load(row + 2 * GW, xa);
+    process(row + GW, xb);
   }
 }
 
@@ -288,11 +444,14 @@ __global__ __launch_bounds__(kThreads) void rownorm_long_kernel(RnArgs a) {
 
 template <typename T, int KIND, int V>
 qk_status LaunchV(const RnArgs& a, hipStream_t st) {
-  constexpr int kSmall = 64 * V * 4, kWave = 64 * V * 16,
+  constexpr int kSmall = 64 * V * 4, kMid = 64 * V * 8, kWave = 64 * V * 16,
                 kBlock = kThreads * V * 16;
   if (a.n <= kSmall) {
     dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
     rownorm_kernel<T, KIND, V, 4, 64><<<grid, kThreads, 0, st>>>(a);
+  } else if (a.n <= kMid) {
+    dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
+    rownorm_kernel<T, KIND, V, 8, 64><<<grid, kThreads, 0, st>>>(a);
   } else if (a.n <= kWave) {
     dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
     rownorm_kernel<T, KIND, V, 16, 64><<<grid, kThreads, 0, st>>>(a);
@@ -306,12 +465,36 @@ qk_status LaunchV(const RnArgs& a, hipStream_t st) {
   return PostLaunch("rownorm");
 }
 
+// Rows of up to 8 vectors per lane with at least two rows per wave: the
+// persistent streamer, two workgroups (eight waves) per CU.
+template <typename T, int KIND>
+bool LaunchStream(const RnArgs& a, hipStream_t st) {
+  constexpr int V = 16 / sizeof(T);
+  // Buffer descriptors take 32-bit extents; rows are at most 64 KB here.
+  auto go = [&](auto kernel) {
+    const int cus = DeviceComputeUnits();
+    const int per_cu = std::min(
+        2, ResidentBlocks(reinterpret_cast<const void*>(kernel), kThreads, 0));
+    const long long waves = static_cast<long long>(per_cu) * cus *
+                            (kThreads / 64);
+    if (a.rows < 2 * waves) return false;
+    kernel<<<dim3(per_cu * cus), kThreads, 0, st>>>(a);
+    return true;
+  };
+  // Rows of more than 8 vectors per lane need two 16-vector buffers (one
+  // wave per SIMD); measured on MI355X the one-shot kernel is faster there.
+  if (a.n <= 64 * V * 4) return go(rownorm_stream_kernel<T, KIND, V, 4>);
+  if (a.n <= 64 * V * 8) return go(rownorm_stream_kernel<T, KIND, V, 8>);
+  return false;
+}
+
 template <typename T, int KIND>
 qk_status LaunchKind(const RnArgs& a, hipStream_t st) {
   constexpr int V = 16 / sizeof(T);
   const bool aligned = (reinterpret_cast<uintptr_t>(a.x) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) &&
                        (static_cast<long long>(a.n) * sizeof(T)) % 16 == 0;
+  if (aligned && LaunchStream<T, KIND>(a, st)) return PostLaunch("rownorm");
   return aligned ? LaunchV<T, KIND, V>(a, st) : LaunchV<T, KIND, 1>(a, st);
 }
 

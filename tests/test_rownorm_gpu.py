@@ -21,7 +21,10 @@ pytestmark = pytest.mark.gpu
 TOL = {"float32": 1e-5, "bfloat16": 8e-3, "float16": 2e-3}
 
 
-def check(got, want, dtype, beta=None):
+def check(got, want, dtype, beta=None, extra=None):
+    """extra: magnitude of intermediate terms whose rounding reaches the
+    output (layer norm: (|x| + |mean|) / std * |gain|, since x - mean
+    carries the rounding error of the mean)."""
     tol = TOL[dtype]
     floor = tol * 1e-3 * np.max(np.abs(want), axis=-1, keepdims=True)
     err = np.abs(got - want)
@@ -29,17 +32,24 @@ def check(got, want, dtype, beta=None):
     # that are added, not with their (possibly cancelling) sum
     mag = np.abs(want) if beta is None else \
         np.abs(want - beta) + np.abs(beta)
+    if extra is not None:
+        mag = mag + extra
     # f16 outputs below 2^-14 are subnormal: one subnormal step is 2^-24
     sub = 2.0 ** -24 if dtype == "float16" else 0.0
     bound = tol * mag + floor + sub
     assert np.all(err <= bound), float(np.max(err / np.maximum(bound, 1e-30)))
 
 
-def run(dev, kind, x, dtype, gain=None, beta=None, eps=1e-6):
+def run(dev, kind, x, dtype, gain=None, beta=None, eps=1e-6, pdtype=None):
+    """pdtype: storage type of gain and beta (default float32); the oracle
+    gets the stored values."""
     dx = torch.from_numpy(x.astype(np.float32)).to(TORCH[dtype]).to(dev)
     xr = dx.float().cpu().numpy().astype(np.float64)  # values as stored
-    dg = None if gain is None else torch.from_numpy(gain).to(dev)
-    dbeta = None if beta is None else torch.from_numpy(beta).to(dev)
+    pt = TORCH[pdtype or "float32"]
+    dg = None if gain is None else torch.from_numpy(gain).to(pt).to(dev)
+    dbeta = None if beta is None else torch.from_numpy(beta).to(pt).to(dev)
+    gain = None if gain is None else dg.float().cpu().numpy()
+    beta = None if beta is None else dbeta.float().cpu().numpy()
     y = qkern.rownorm(dx, kind, eps=eps, gain=dg, beta=dbeta)
     torch.cuda.synchronize()
     got = y.float().cpu().numpy().astype(np.float64)
@@ -47,11 +57,15 @@ def run(dev, kind, x, dtype, gain=None, beta=None, eps=1e-6):
         want = O.rms_norm(xr, gain, eps)
     elif kind == RownormKind.LAYER:
         want = O.layer_norm(xr, eps, gain, beta)
+        mu = xr.mean(axis=-1, keepdims=True)
+        inv = 1.0 / np.sqrt(((xr - mu) ** 2).mean(axis=-1, keepdims=True) + eps)
+        extra = (np.abs(xr) + np.abs(mu)) * inv * \
+            (1.0 if gain is None else np.abs(gain))
     else:
         want = O.softmax(xr)
     # compare against the oracle rounded once to the output type
     check(got, O.round_to(want, dtype) if dtype != "float32" else want, dtype,
-          beta)
+          beta, extra if kind == RownormKind.LAYER else None)
 
 
 SHAPES = [(1, 1), (3, 7), (5, 64), (7, 1000), (2, 129), (4, 4096),
@@ -70,6 +84,26 @@ def test_rownorm_shapes(dev, kind, dtype):
         if kind == RownormKind.LAYER:
             beta = (0.1 * rng.standard_normal(n)).astype(np.float32)
         run(dev, kind, x, dtype, gain, beta, 1e-6 if kind == 0 else 1e-5)
+
+
+@pytest.mark.parametrize("kind", list(RownormKind))
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+def test_rownorm_many_rows(dev, kind, dtype):
+    """Enough rows for the persistent streaming kernel (several rows per
+    wave, a ragged last round), for each register size class, with gains
+    and offsets of the row type and of f32."""
+    rng = np.random.default_rng(10 + int(kind))
+    cases = [(4099, 1000, "float32"), (4101, 4096, dtype),
+             (4097, 8192 if dtype != "float32" else 4104, "float32")]
+    for rows, n, pdtype in cases:
+        x = rng.standard_normal((rows, n)) * (2.0 if kind == 2 else 1.0) + 0.3
+        gain = beta = None
+        if kind != RownormKind.SOFTMAX:
+            gain = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        if kind == RownormKind.LAYER:
+            beta = (0.1 * rng.standard_normal(n)).astype(np.float32)
+        run(dev, kind, x, dtype, gain, beta, 1e-6 if kind == 0 else 1e-5,
+            pdtype)
 
 
 def test_rownorm_no_gain_and_leading_dims(dev):
