@@ -93,6 +93,11 @@ struct QuantProblem {
 
 qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream);
 
+// Quantized matmul for 2..64 rows of x (qskinny.hip): int4 u32x8, bf16,
+// group 64.
+bool QSkinnyApplies(const QuantProblem& p);
+qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream);
+
 // Dequantizing MFMA GEMM (qgemm.hip) for more than four rows of x.
 bool QGemmApplies(const QuantProblem& p);
 qk_status LaunchQGemm(const QuantProblem& p, hipStream_t stream);

@@ -1046,9 +1046,12 @@ qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream) {
   }
   QmvArgs a = MakeArgs(p);
   const int m = static_cast<int>(p.m);
-  // Beyond four rows, like the reference's linear() (ROWS_MAX = 4,
-  // examples/llm/qwen3.py:215-230): dequantize to x's type and multiply,
-  // fused into one MFMA GEMM.
+  // Beyond four rows the reference's linear() (ROWS_MAX = 4,
+  // examples/llm/qwen3.py:215-230) dequantizes to x's type and multiplies.
+  // Up to 64 rows of int4 u32x8 codes stream through MFMA with the codes
+  // kept factored per group (qskinny.hip); otherwise dequantize and
+  // multiply in one fused MFMA GEMM (qgemm.hip).
+  if (m > 4 && QSkinnyApplies(p)) return LaunchQSkinny(p, stream);
   if (m > 4 && QGemmApplies(p)) return LaunchQGemm(p, stream);
   if (m <= 4) {
     const int cus = DeviceComputeUnits();

@@ -1,0 +1,420 @@
+// Quantized matmul for a few rows of x (5 <= M <= 64 as routed; the kernel
+// takes 1..64): y[M, N] = x[M, K] W^T with W int4 (u32x8 words), bf16 x /
+// scale / offset, group size 64: the batched-decode and short-prefill
+// shapes. The reference's linear() (examples/llm/qwen3.py:215-230)
+// dequantizes W to x's type for more than ROWS_MAX = 4 rows and multiplies;
+// this kernel keeps the codes factored as its _matvec_int4 does
+// (qwen3.py:233-267: y = s * sum(x q) + b * sum(x) per group), which skips
+// the bf16 rounding of the weights and agrees with the dequantized product
+// within that rounding.
+//
+// Design (MI355X-first). The work is HBM-bound (N K / 2 bytes of codes
+// against 2 M N K flops), so the codes are streamed once:
+//  - A workgroup owns NR = 16 NB weight rows and splits K over its KW waves
+//    (reduced through LDS at the end). Each wave walks its K slice in
+//    sub-chunks of CG groups: the sub-chunk's codes are read as contiguous
+//    row segments (32 CG bytes per row, 16 bytes per lane) and reach the
+//    MFMA layout through a wave-private LDS buffer (a wave's LDS
+//    operations run in order, so each sub-chunk is written over the last
+//    after its final read). Scales, offsets and the sub-chunk's x travel
+//    with the codes: the next sub-chunk is requested as a whole while the
+//    current one is computed, in consumption order, so the in-order memory
+//    counter never waits for data that is not needed yet. Sub-chunks past
+//    a wave's slice are requested through out-of-range offsets (zeros, no
+//    memory traffic), so no load is conditional.
+//  - v_mfma_f32_16x16x32_bf16 with A = 16 rows of x and B = 16 weight rows.
+//    Lane l takes the code words 2 (l / 16) and 2 (l / 16) + 1 of a group
+//    (one 8-byte LDS read) for the group's two MFMAs, so every MFMA
+//    multiplies K values of one group only and the group's scale can be
+//    applied after it. x is loaded as the matching 32 bytes per lane.
+//  - Codes become bf16 pairs (128 + q_a, 128 + q_b) with one v_and_or_b32
+//    (nibbles s and s + 4 of a word; 0x4300 | q is exactly 128 + q); x is
+//    permuted with v_perm_b32 into the same K order.
+//  - Per group: tmp = sum x (128 + q) and xs = sum x (one MFMA against a
+//    constant 1.0 operand, which lands xs in the accumulator layout), then
+//    acc += s tmp + (b - 128 s) xs.
+//  - Rows past M or N read zeros through buffer descriptors and are not
+//    stored.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdlib>
+
+#include "qk_device.h"
+#include "qk_internal.h"
+
+namespace qk {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+struct SkArgs {
+  const void* x;
+  const void* codes;
+  const void* scales;
+  const void* biases;
+  void* y;
+  int m, n, k;
+  int groups;  // k / 64
+  int has_bias;
+  int chunks;  // 256-K sub-chunks per wave
+};
+
+constexpr int kNonTemporal = 2;
+constexpr int kOut = 0x7FFF0000;             // an offset past every extent
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t Rsrc(const void* p,
+                                                       int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
+                                           bytes, 0x00020000);
+}
+
+// x (8 consecutive bf16, as loaded) -> the pair order of a code word:
+// (x0, x4), (x1, x5), (x2, x6), (x3, x7).
+__device__ __forceinline__ bf16x8 XPairs(const u32x4& v) {
+  constexpr uint32_t kLoLo = 0x05040100u, kHiHi = 0x07060302u;
+  const u32x4 p = {__builtin_amdgcn_perm(v[2], v[0], kLoLo),
+                   __builtin_amdgcn_perm(v[2], v[0], kHiHi),
+                   __builtin_amdgcn_perm(v[3], v[1], kLoLo),
+                   __builtin_amdgcn_perm(v[3], v[1], kHiHi)};
+  return __builtin_bit_cast(bf16x8, p);
+}
+
+// One u32x8 code word -> bf16 (128 + q) in the same order.
+__device__ __forceinline__ bf16x8 CodePairs(uint32_t w, uint32_t mask,
+                                            uint32_t bias) {
+  const uint64_t v = w;  // the high half is never used
+  const u32x4 p = {(w & mask) | bias,
+                   (static_cast<uint32_t>(shr64<4>(v)) & mask) | bias,
+                   (static_cast<uint32_t>(shr64<8>(v)) & mask) | bias,
+                   (static_cast<uint32_t>(shr64<12>(v)) & mask) | bias};
+  return __builtin_bit_cast(bf16x8, p);
+}
+
+// 8 bytes of int8 codes -> bf16 (exact: integers up to 256 are bf16
+// values); signed symmetric codes are first flipped to q + 128.
+template <int PACK>
+__device__ __forceinline__ bf16x8 CodeBytes(uint32_t w0, uint32_t w1) {
+  if (PACK == QK_PACK_S8_SYM) w0 ^= 0x80808080u, w1 ^= 0x80808080u;
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    r[e] = from_f32<bf16>(static_cast<float>((w0 >> (8 * e)) & 0xFFu));
+    r[4 + e] = from_f32<bf16>(static_cast<float>((w1 >> (8 * e)) & 0xFFu));
+  }
+  return r;
+}
+
+template <int PACK, int MB, int NB, int KW, int CG>
+__global__ __launch_bounds__(KW * 64) void qmm_skinny_kernel(SkArgs a) {
+  constexpr bool kInt4 = PACK == QK_PACK_U32X8;
+  constexpr int GB = kInt4 ? 32 : 64;   // code bytes per group per row
+  constexpr int NR = 16 * NB;           // weight rows per workgroup
+  constexpr int SEG = GB * CG;          // code bytes per row per sub-chunk
+  constexpr int LPR = SEG / 16;         // lanes per row in a code load
+  constexpr int RPL = 64 / LPR;         // rows per code load
+  constexpr int CL = NR / RPL;          // code loads per sub-chunk
+  constexpr int kRow = SEG + 16;        // LDS row stride (padded)
+  constexpr int kBuf = NR * kRow;
+  constexpr int kWaveBytes = kBuf + 2 * NR * CG * 2;
+  constexpr int kPartBytes = KW * (16 * MB) * (NR + 1) * 4;
+  static_assert(CL >= 1 && NR % RPL == 0, "tile");
+  __shared__ __attribute__((aligned(16)))
+  unsigned char lds[KW * kWaveBytes > kPartBytes ? KW * kWaveBytes
+                                                 : kPartBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q16 = lane >> 4, l16 = lane & 15;
+  const int n0 = blockIdx.x * NR;
+  const int G = a.groups;
+  unsigned char* const code_buf = lds + wave * kWaveBytes;
+  uint16_t* const sb_buf = reinterpret_cast<uint16_t*>(code_buf + kBuf);
+
+  const int row_bytes = kInt4 ? a.k / 2 : a.k;
+  const auto crs = Rsrc(a.codes, a.n * row_bytes);
+  const auto xrs = Rsrc(a.x, a.m * a.k * 2);
+  const auto srs = Rsrc(a.scales, a.n * G * 2);
+  const auto brs = Rsrc(a.biases, a.has_bias ? a.n * G * 2 : 0);
+
+  // Code loads: load i, lane l -> row RPL i + l / LPR, 16 bytes at
+  // 16 (l % LPR) of the row's sub-chunk segment.
+  int cvo[CL];
+#pragma unroll
+  for (int i = 0; i < CL; ++i) {
+    const int r = n0 + RPL * i + lane / LPR;
+    cvo[i] = r < a.n ? r * row_bytes + 16 * (lane % LPR) : kOut;
+  }
+  // Scale/offset loads: lane l < NR loads the CG scales and the CG offsets
+  // of row l (two loads; one descriptor per array).
+  const bool sb_lane = lane < NR;
+  const int sb_row = n0 + lane;
+  const int svo = (sb_lane && sb_row < a.n) ? sb_row * G * 2 : kOut;
+  // x loads: lane l -> row 16 mb + l % 16, 32 bytes at K offset 16 (l / 16)
+  // of each group.
+  int xvo[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int r = 16 * mb + l16;
+    xvo[mb] = r < a.m ? r * a.k * 2 + 32 * q16 : kOut;
+  }
+
+  struct Chunk {
+    u32x4 c[CL];
+    uint32_t s[CG / 2], b[CG / 2];
+    u32x4 x[CG][MB][2];
+  };
+  // `skip`: sub-chunks past the slice read zeros (offsets past the extents).
+  auto load = [&](int ch, bool skip, Chunk& t) {
+    const int oob = skip ? kOut : 0;
+#pragma unroll
+    for (int i = 0; i < CL; ++i)
+      t.c[i] = __builtin_amdgcn_raw_buffer_load_b128(
+          crs, cvo[i] + oob, ch * SEG, kNonTemporal);
+    if constexpr (CG == 4) {
+      const u32x2 vs = __builtin_amdgcn_raw_buffer_load_b64(srs, svo + oob,
+                                                            ch * 8, 0);
+      const u32x2 vb = __builtin_amdgcn_raw_buffer_load_b64(brs, svo + oob,
+                                                            ch * 8, 0);
+      t.s[0] = vs[0], t.s[1] = vs[1], t.b[0] = vb[0], t.b[1] = vb[1];
+    } else {
+      t.s[0] = __builtin_amdgcn_raw_buffer_load_b32(srs, svo + oob, ch * 4, 0);
+      t.b[0] = __builtin_amdgcn_raw_buffer_load_b32(brs, svo + oob, ch * 4, 0);
+    }
+#pragma unroll
+    for (int gg = 0; gg < CG; ++gg)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+          t.x[gg][mb][t2] = __builtin_amdgcn_raw_buffer_load_b128(
+              xrs, xvo[mb] + oob + 16 * t2, (ch * CG + gg) * 128, 0);
+  };
+
+  f32x4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const uint32_t kMask = vgpr_const(0x000F000Fu);
+  const uint32_t kBias = vgpr_const(0x43004300u);
+  const bf16x8 ones = __builtin_bit_cast(
+      bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+
+  auto process = [&](const Chunk& t) {
+    // codes and scales into the wave's LDS buffer
+#pragma unroll
+    for (int i = 0; i < CL; ++i)
+      *reinterpret_cast<u32x4*>(code_buf + (RPL * i + lane / LPR) * kRow +
+                                16 * (lane % LPR)) = t.c[i];
+    if (sb_lane) {  // [scales | offsets][row][group]
+      uint32_t* ds = reinterpret_cast<uint32_t*>(sb_buf + lane * CG);
+      uint32_t* db = reinterpret_cast<uint32_t*>(sb_buf + (NR + lane) * CG);
+#pragma unroll
+      for (int h = 0; h < CG / 2; ++h) ds[h] = t.s[h], db[h] = t.b[h];
+    }
+#pragma unroll
+    for (int gg = 0; gg < CG; ++gg) {
+      bf16x8 xa[MB][2];
+      f32x4 xs[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        xs[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) {
+          // int4: x in the pair order of the code words; int8: as loaded
+          xa[mb][t2] = kInt4 ? XPairs(t.x[gg][mb][t2])
+                             : __builtin_bit_cast(bf16x8, t.x[gg][mb][t2]);
+          xs[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[mb][t2], ones,
+                                                           xs[mb], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int row = 16 * nb + l16;
+        bf16x8 b0, b1;
+        if constexpr (kInt4) {
+          const u32x2 w = *reinterpret_cast<const u32x2*>(
+              code_buf + row * kRow + gg * GB + 8 * q16);
+          b0 = CodePairs(w[0], kMask, kBias);
+          b1 = CodePairs(w[1], kMask, kBias);
+        } else {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(
+              code_buf + row * kRow + gg * GB + 16 * q16);
+          b0 = CodeBytes<PACK>(w[0], w[1]);
+          b1 = CodeBytes<PACK>(w[2], w[3]);
+        }
+        const float sc = __uint_as_float(
+            static_cast<uint32_t>(sb_buf[row * CG + gg]) << 16);
+        const float of = __uint_as_float(
+            static_cast<uint32_t>(sb_buf[(NR + row) * CG + gg]) << 16);
+        // int4 and signed int8 codes enter as q + 128
+        const float off = PACK == QK_PACK_U8 ? of : of - 128.f * sc;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              xa[mb][0], b0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[mb][1], b1, tmp, 0,
+                                                        0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[mb][nb][r] =
+                fmaf(sc, tmp[r], fmaf(off, xs[mb][r], acc[mb][nb][r]));
+        }
+      }
+    }
+  };
+
+  // Two sub-chunks in registers: A and B alternate; every load is issued
+  // (past the slice as zeros) so the wait counts follow the ping-pong.
+  const int kc0 = wave * a.chunks;
+  Chunk A, B;
+  load(kc0, false, A);
+  for (int c = 0; c < a.chunks; c += 2) {
+    load(kc0 + c + 1, c + 1 >= a.chunks, B);
+    process(A);
+    load(kc0 + c + 2, c + 2 >= a.chunks, A);
+    if (c + 1 < a.chunks) process(B);
+  }
+
+  // Reduce the KW partial tiles and store rows < M, columns < N.
+  __syncthreads();
+  float* part = reinterpret_cast<float*>(lds);
+  constexpr int TM = 16 * MB, TS = NR + 1;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        part[(wave * TM + 16 * mb + 4 * q16 + r) * TS + 16 * nb + l16] =
+            acc[mb][nb][r];
+  __syncthreads();
+  bf16* Y = static_cast<bf16*>(a.y);
+  for (int e = threadIdx.x; e < TM * NR; e += KW * 64) {
+    const int r = e / NR, c = e % NR;
+    if (r >= a.m || n0 + c >= a.n) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < KW; ++w) v += part[(w * TM + r) * TS + c];
+    Y[static_cast<long long>(r) * a.n + n0 + c] = from_f32<bf16>(v);
+  }
+}
+
+}  // namespace
+
+bool QSkinnyApplies(const QuantProblem& p) {
+  const int64_t m = p.m;
+  const bool int4 = p.bits == 4 && p.packing == QK_PACK_U32X8;
+  const bool int8 = p.bits == 8 && (p.packing == QK_PACK_U8 ||
+                                    p.packing == QK_PACK_S8_SYM);
+  const int64_t row_bytes = int4 ? p.k / 2 : p.k;
+  return m >= 1 && m <= (int4 ? 64 : 32) && (int4 || int8) && p.group == 64 &&
+         p.x_dtype == QK_BF16 && p.scale_dtype == QK_BF16 &&
+         (!p.has_bias || p.bias_dtype == QK_BF16) && p.k % 1024 == 0 &&
+         p.k > 0 && p.n > 0 && p.n * row_bytes < (int64_t{1} << 31) &&
+         m * p.k * 2 < (int64_t{1} << 31) &&
+         p.n * (p.k / 64) * 2 < (int64_t{1} << 31) &&
+         reinterpret_cast<uintptr_t>(p.x) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(p.codes) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(p.scales) % 8 == 0 &&
+         (!p.has_bias || reinterpret_cast<uintptr_t>(p.biases) % 8 == 0);
+}
+
+qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream) {
+  SkArgs a;
+  a.x = p.x;
+  a.codes = p.codes;
+  a.scales = p.scales;
+  a.biases = p.has_bias ? p.biases : nullptr;
+  a.y = p.y;
+  a.m = static_cast<int>(p.m);
+  a.n = static_cast<int>(p.n);
+  a.k = static_cast<int>(p.k);
+  a.groups = a.k / 64;
+  a.has_bias = p.has_bias ? 1 : 0;
+  const int cus = DeviceComputeUnits();
+  const int mb = (a.m + 15) / 16;
+  // Sub-chunks of 4 groups (2 for more than 32 rows of x, to bound the
+  // registers); 32 weight rows per workgroup when that still gives every
+  // CU one (16 for more than 32 rows of x); eight waves split K (fewer
+  // when K is short), each walking k / KW.
+  const bool int4 = p.packing == QK_PACK_U32X8;
+  const int cg = int4 && mb <= 2 ? 4 : 2;
+  bool wide = (a.n + 31) / 32 >= cus && mb <= (int4 ? 2 : 1);
+  // QK_SKINNY_ROWS=16|32 forces the weight rows per workgroup (tuning).
+  static const int forced_rows = [] {
+    const char* v = std::getenv("QK_SKINNY_ROWS");
+    return v == nullptr ? 0 : std::atoi(v);
+  }();
+  if (forced_rows == 16) wide = false;
+  if (forced_rows == 32 && mb <= (int4 ? 2 : 1)) wide = true;
+  const int nr = wide ? 32 : 16;
+  const dim3 grid((a.n + nr - 1) / nr);
+  // The most waves per workgroup (8, 4 or 2) for which every workgroup is
+  // resident at once (no second, partly empty round) and k splits evenly.
+  auto go = [&](auto k8, auto k4, auto k2) {
+    auto fits = [&](const void* f, int waves) {
+      return a.k % (waves * 64 * cg) == 0 &&
+             static_cast<int64_t>(ResidentBlocks(f, waves * 64, 0)) * cus >=
+                 grid.x;
+    };
+    int kw = 2;
+    if (fits(reinterpret_cast<const void*>(k8), 8))
+      kw = 8;
+    else if (fits(reinterpret_cast<const void*>(k4), 4))
+      kw = 4;
+    a.chunks = a.k / kw / (64 * cg);  // k % 1024 == 0: kw = 2 always divides
+    if (kw == 8)
+      k8<<<grid, 8 * 64, 0, stream>>>(a);
+    else if (kw == 4)
+      k4<<<grid, 4 * 64, 0, stream>>>(a);
+    else
+      k2<<<grid, 2 * 64, 0, stream>>>(a);
+  };
+#define QK_SKINNY(P, MB, NB, CG)                                         \
+  go(qmm_skinny_kernel<P, MB, NB, 8, CG>,                                \
+     qmm_skinny_kernel<P, MB, NB, 4, CG>, qmm_skinny_kernel<P, MB, NB, 2, CG>)
+  if (p.packing == QK_PACK_U32X8) {
+    switch (mb) {
+      case 1:
+        if (wide) QK_SKINNY(QK_PACK_U32X8, 1, 2, 4);
+        else QK_SKINNY(QK_PACK_U32X8, 1, 1, 4);
+        break;
+      case 2:
+        if (wide) QK_SKINNY(QK_PACK_U32X8, 2, 2, 4);
+        else QK_SKINNY(QK_PACK_U32X8, 2, 1, 4);
+        break;
+      case 3:
+        QK_SKINNY(QK_PACK_U32X8, 3, 1, 2);
+        break;
+      default:
+        QK_SKINNY(QK_PACK_U32X8, 4, 1, 2);
+        break;
+    }
+  } else if (p.packing == QK_PACK_U8) {
+    if (mb == 1) {
+      if (wide) QK_SKINNY(QK_PACK_U8, 1, 2, 2);
+      else QK_SKINNY(QK_PACK_U8, 1, 1, 2);
+    } else {
+      QK_SKINNY(QK_PACK_U8, 2, 1, 2);
+    }
+  } else {
+    if (mb == 1) {
+      if (wide) QK_SKINNY(QK_PACK_S8_SYM, 1, 2, 2);
+      else QK_SKINNY(QK_PACK_S8_SYM, 1, 1, 2);
+    } else {
+      QK_SKINNY(QK_PACK_S8_SYM, 2, 1, 2);
+    }
+  }
+#undef QK_SKINNY
+  return PostLaunch("qmm_skinny");
+}
+
+}  // namespace qk

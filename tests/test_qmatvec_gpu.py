@@ -117,6 +117,32 @@ def test_qmatvec_single_row_paths(dev, packing, k):
             check_matvec(y.float().cpu().numpy().astype(np.float64), x, w)
 
 
+@pytest.mark.parametrize("mnk", [(5, 300, 4096), (8, 77, 1024),
+                                 (16, 4096, 4096), (32, 1000, 512),
+                                 (33, 64, 1024), (40, 520, 12288),
+                                 (64, 2048, 2048)])
+@pytest.mark.parametrize("packing", [Packing.U32X8, Packing.U8,
+                                     Packing.S8_SYM])
+def test_qmatvec_few_rows(dev, mnk, packing):
+    """5..64 rows of bf16 x with group-64 int4 u32x8 or int8 codes (the
+    streaming MFMA kernel up to 64 / 32 rows, the dequantizing paths
+    beyond): ragged N, one to four 16-row blocks, long K, with and without
+    offsets, elementwise against the float64 oracle."""
+    m, n, k = mnk
+    rng = np.random.default_rng(m * 7 + n)
+    for has_bias in (True, False):
+        dc, ds, db, w, *_ = make_weights(rng, n, k, packing, 64,
+                                         has_bias=has_bias)
+        x = O.round_to(rng.standard_normal((m, k)), "bfloat16").astype(
+            np.float32)
+        y = qkern.qmatvec(torch.from_numpy(x).to(torch.bfloat16).to(dev),
+                          dc.to(dev), ds.to(dev),
+                          None if db is None else db.to(dev),
+                          packing=packing)
+        torch.cuda.synchronize()
+        check_matvec(y.float().cpu().numpy().astype(np.float64), x, w)
+
+
 def test_qmatvec_leading_dims_and_no_bias(dev):
     rng = np.random.default_rng(5)
     dc, ds, _, w, *_ = make_weights(rng, 40, 256, Packing.U32X8, 64,
