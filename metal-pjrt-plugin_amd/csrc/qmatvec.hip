@@ -822,6 +822,204 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
   }
 }
 
+// The int8 decode path: M = 1, bf16 x, u8 or s8 codes, group size 64, bf16
+// scales/offsets, k a multiple of 4096 (CPL = k / 1024 16-byte chunks per
+// lane, a multiple of 4; 4, 8 or 12 here). Lane l reads chunk 64 j + l, so every wave-wide
+// load is 1 KB of contiguous codes; chunk 64 j + l belongs to group
+// 16 j + l / 4, so the four lanes of a quad hold the four chunks of the
+// same groups. After a two-step DPP transpose inside the quad each lane
+// holds the full dot product of one group per four chunks (lane l: chunk
+// 4 u + l % 4), so it loads one scale and one offset per four chunks.
+// Codes convert exactly to bf16 (integers up to 256; signed codes are
+// flipped to q + 128 and the 128 removed per group) and meet x pairs in
+// v_dot2_f32_bf16. Rows are reduced four at a time as in the int4 kernel.
+template <int PACK, int CPL, int D>
+__global__ __launch_bounds__(kStreamThreads) void qmv_m1_i8_kernel(QmvArgs a) {
+  static_assert(CPL % 4 == 0, "quads of chunks");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int cpr = 64 * CPL;   // 16-byte chunks per row
+  constexpr int U = CPL / 4;      // groups per lane
+  constexpr int groups = cpr / 4;
+  u32x4* xl = reinterpret_cast<u32x4*>(smem);  // x as loaded, [2 cpr]
+  const int lane = threadIdx.x & 63;
+  const int q4 = lane & 3;
+  const int gw = __builtin_amdgcn_readfirstlane(
+      blockIdx.x * (kStreamThreads / 64) + (threadIdx.x >> 6));
+  const int GW = gridDim.x * (kStreamThreads / 64);
+
+  const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(a.codes), (short)0, a.n * a.row_bytes, 0x00020000);
+  const int sb_bytes = a.n * groups * 2;
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(a.scales), (short)0, sb_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(a.biases), (short)0, a.has_bias ? sb_bytes : 0,
+      0x00020000);
+  // Lane l keeps, for u < U, the group of chunk 64 (4 u + l % 4) + l:
+  // 16 (4 u + l % 4) + l / 4.
+  const int cvoff = lane * 16;
+  const int svoff = (16 * q4 + (lane >> 2)) * 2;
+  constexpr int kNonTemporal = 2;
+
+  struct Slot {
+    u32x4 w[CPL];
+    uint16_t s[U], b[U];
+  };
+  auto load_row = [&](int row, Slot& r, bool skip = false) {
+    const int co = skip ? 0 : row * a.row_bytes;
+    const int so = skip ? 0 : row * groups * 2;
+    const int oob = skip ? 0x7FFF0000 : 0;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      r.w[j] = __builtin_amdgcn_raw_buffer_load_b128(
+          crs, cvoff + oob + 1024 * j, co, kNonTemporal);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      r.s[u] = __builtin_amdgcn_raw_buffer_load_b16(srs, svoff + oob + 128 * u,
+                                                    so, 0);
+      r.b[u] = __builtin_amdgcn_raw_buffer_load_b16(brs, svoff + oob + 128 * u,
+                                                    so, 0);
+    }
+  };
+
+  // x first (loads complete in order), then the first rows; x goes through
+  // LDS once per workgroup.
+  constexpr int XV = 2 * cpr;  // 16-byte vectors of x
+  constexpr int XPT = (XV + kStreamThreads - 1) / kStreamThreads;
+  u32x4 xraw[XPT];
+  const u32x4* X = static_cast<const u32x4*>(a.x);
+#pragma unroll
+  for (int q = 0; q < XPT; ++q) {
+    const int c = threadIdx.x + q * kStreamThreads;
+    if (c < XV) xraw[q] = X[c];
+  }
+  Slot buf[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int r = gw + d * GW;
+    load_row(r, buf[d], r >= a.n);
+  }
+#pragma unroll
+  for (int q = 0; q < XPT; ++q) {
+    const int c = threadIdx.x + q * kStreamThreads;
+    if (c < XV) xl[c] = xraw[q];
+  }
+  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  // The lane's x: chunk 64 j + l covers x[16 (64 j + l) ...], two vectors.
+  u32x4 xr[CPL][2];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) xr[j][h] = xl[2 * (64 * j + lane) + h];
+  const uint32_t ones = 0x3F803F80u;  // bf16 (1, 1)
+
+  // Quad transpose: lane l gets the quad sum of v[4 u + l % 4].
+  auto quad4 = [&](float v0, float v1, float v2, float v3) {
+    const bool b0 = lane & 1, b1 = lane & 2;
+    const float v01 = (b0 ? v1 : v0) + dpp_f32<0xB1>(b0 ? v0 : v1);
+    const float v23 = (b0 ? v3 : v2) + dpp_f32<0xB1>(b0 ? v2 : v3);
+    return (b1 ? v23 : v01) + dpp_f32<0x4E>(b1 ? v01 : v23);
+  };
+  float xsum[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float cs[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      float sacc = 0.f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          sacc = __builtin_amdgcn_fdot2_f32_bf16(
+              AsBf16x2(xr[4 * u + jj][h][e]), AsBf16x2(ones), sacc, false);
+      cs[jj] = sacc;
+    }
+    xsum[u] = quad4(cs[0], cs[1], cs[2], cs[3]);
+  }
+
+  // Two codes (bytes of w at 8 c and 8 c + 8) as a bf16 pair.
+  auto code2 = [](uint32_t w, int c) {
+    const float lo = static_cast<float>((w >> (16 * c)) & 0xFFu);
+    const float hi = static_cast<float>((w >> (16 * c + 8)) & 0xFFu);
+    const bf16x2 p = {from_f32<bf16>(lo), from_f32<bf16>(hi)};
+    return p;
+  };
+  auto row_acc = [&](const Slot& r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float dj[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int j = 4 * u + jj;
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          uint32_t w = r.w[j][i];
+          if (PACK == QK_PACK_S8_SYM) w ^= 0x80808080u;
+#pragma unroll
+          for (int c = 0; c < 2; ++c)
+            d = __builtin_amdgcn_fdot2_f32_bf16(
+                code2(w, c), AsBf16x2(xr[j][i >> 1][2 * (i & 1) + c]), d,
+                false);
+        }
+        dj[jj] = d;
+      }
+      const float dg = quad4(dj[0], dj[1], dj[2], dj[3]);
+      const float sc = __uint_as_float(static_cast<uint32_t>(r.s[u]) << 16);
+      const float of = __uint_as_float(static_cast<uint32_t>(r.b[u]) << 16);
+      const float off = PACK == QK_PACK_S8_SYM ? of - 128.f * sc : of;
+      acc = fmaf(sc, dg, fmaf(off, xsum[u], acc));
+    }
+    return acc;
+  };
+
+  bf16* Y = static_cast<bf16*>(a.y);
+  int row = gw;
+  static_assert(D == 2 || D % 4 == 0, "rows are reduced four at a time");
+  constexpr int DA = D < 4 ? 4 : D;
+  for (; row + (2 * D - 1) * GW < a.n; row += D * GW) {
+    float acc[DA] = {};
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      acc[d] = row_acc(buf[d]);
+      load_row(row + (d + D) * GW, buf[d]);
+    }
+#pragma unroll
+    for (int q = 0; q < DA; q += 4) {
+      const float v = wave_sum4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3],
+                                lane);
+      if (lane < 4 && q + lane < D) Y[row + (q + lane) * GW] = from_f32<bf16>(v);
+    }
+  }
+  for (; row < a.n; row += D * GW) {
+    float acc[DA] = {};
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int r = row + d * GW;
+      if (r < a.n) {
+        acc[d] = row_acc(buf[d]);
+        const int nr = r + D * GW;
+        if (nr < a.n) load_row(nr, buf[d]);
+      }
+    }
+    if (row + GW >= a.n) {
+      const float v = wave_sum_dpp(acc[0]);
+      if (lane == 0) Y[row] = from_f32<bf16>(v);
+    } else {
+#pragma unroll
+      for (int q = 0; q < DA; q += 4) {
+        const float v = wave_sum4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3],
+                                  lane);
+        const int rr = row + (q + (lane & 3)) * GW;
+        if (lane < 4 && q + lane < D && rr < a.n) Y[rr] = from_f32<bf16>(v);
+      }
+    }
+  }
+}
+
 // QK_QMV_WG_PER_CU=<n> sets the workgroups per CU of the streaming
 // kernels, within what stays resident (tuning only); 0 when unset.
 int QmvWgPerCu() {
@@ -892,6 +1090,36 @@ bool LaunchM1(const QmvArgs& a, int cus, hipStream_t stream, qk_status* st) {
   }
 }
 
+template <int PACK>
+bool LaunchM1I8(const QmvArgs& a, int cus, hipStream_t stream, qk_status* st) {
+  const int cpr = a.row_bytes / 16;  // int8: row_bytes = k
+  if (a.m != 1 || a.group != 64 || cpr % 256 != 0) return false;
+  if (static_cast<int64_t>(a.n) * a.row_bytes >= (int64_t{1} << 31))
+    return false;
+  const int cpl = cpr / 64;
+  const size_t lds = static_cast<size_t>(2 * cpr) * 16;
+  const int need = (a.n + 3) / 4;
+  auto go = [&](auto kernel) {
+    const int resident = ResidentBlocks(reinterpret_cast<const void*>(kernel),
+                                        kStreamThreads, lds);
+    const int per_cu = std::min(QmvWgPerCu() ? QmvWgPerCu() : 2, resident);
+    const int grid = std::max(1, std::min(need, cus * per_cu));
+    kernel<<<grid, kStreamThreads, lds, stream>>>(a);
+    *st = PostLaunch("qmv_m1_i8");
+    return true;
+  };
+  switch (cpl) {
+    case 4:
+      return go(qmv_m1_i8_kernel<PACK, 4, 2>);
+    case 8:
+      return go(qmv_m1_i8_kernel<PACK, 8, 2>);
+    case 12:
+      return go(qmv_m1_i8_kernel<PACK, 12, 2>);
+    default:
+      return false;
+  }
+}
+
 template <int PACK, typename XT, int MT, bool kBf16SB>
 qk_status LaunchStreamMT(QmvArgs a, int cpl, int cus, hipStream_t st) {
   const int cpr = a.row_bytes / 16;
@@ -938,6 +1166,9 @@ bool LaunchStream(const QmvArgs& a, int cus, hipStream_t stream,
   const bool sb16 = a.sdt == QK_BF16 && (!a.has_bias || a.bdt == QK_BF16);
   const bool fast = sb16 && std::is_same<XT, bf16>::value;
   const int mt = !fast ? 4 : a.m <= 1 ? 1 : a.m <= 2 ? 2 : 4;
+  if constexpr (PACK == QK_PACK_U8 || PACK == QK_PACK_S8_SYM) {
+    if (fast && a.m == 1 && LaunchM1I8<PACK>(a, cus, stream, st)) return true;
+  }
   const size_t lds = static_cast<size_t>(mt) * cpr * (64 + 4);
   if (lds > 64 * 1024) return false;
   if (fast && a.m == 1 && ChunkTraits<PACK>::kInt4 && lds <= 64 * 1024 &&

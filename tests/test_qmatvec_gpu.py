@@ -89,12 +89,13 @@ def test_qmatvec_small(dev, packing, xdt):
         check_matvec(y.float().cpu().numpy().astype(np.float64), x, w)
 
 
-@pytest.mark.parametrize("packing", [Packing.U32X8, Packing.BYTE_HALFSPLIT])
+@pytest.mark.parametrize("packing", list(Packing))
 @pytest.mark.parametrize("k", [4096, 8192, 12288, 16384])
 def test_qmatvec_single_row_paths(dev, packing, k):
-    """M = 1, bf16 x, group 64: the decode kernel (x loaded per lane), for
-    every chunks-per-lane count, ragged N, with and without offsets; an x
-    that is not 16-byte aligned is rejected."""
+    """M = 1, bf16 x, group 64: the int4 and int8 decode kernels for every
+    chunks-per-lane count (the general streaming kernel beyond), ragged N,
+    with and without offsets; an x that is not 16-byte aligned is
+    rejected."""
     rng = np.random.default_rng(k + int(packing))
     for n, has_bias in ((300, True), (77, False)):
         dc, ds, db, w, *_ = make_weights(rng, n, k, packing, 64,
