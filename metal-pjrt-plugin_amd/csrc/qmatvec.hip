@@ -1156,19 +1156,19 @@ template <int PACK, typename XT>
 bool LaunchStream(const QmvArgs& a, int cus, hipStream_t stream,
                   qk_status* st) {
   const int cpr = a.row_bytes / 16;
+  // The decode case (bf16 x, bf16 scales) gets kernels per row count;
+  // everything else runs the four-row kernel with masked rows.
+  const bool sb16 = a.sdt == QK_BF16 && (!a.has_bias || a.bdt == QK_BF16);
+  const bool fast = sb16 && std::is_same<XT, bf16>::value;
+  if constexpr (PACK == QK_PACK_U8 || PACK == QK_PACK_S8_SYM) {
+    if (fast && a.m == 1 && LaunchM1I8<PACK>(a, cus, stream, st)) return true;
+  }
   int cpl = (cpr + 63) / 64;
   if (cpl > 8 || a.m > 4) return false;
   if (cpl == 3) cpl = 4;
   if (cpl == 5) cpl = 6;
   if (cpl == 7) cpl = 8;
-  // The decode case (bf16 x, bf16 scales) gets kernels per row count;
-  // everything else runs the four-row kernel with masked rows.
-  const bool sb16 = a.sdt == QK_BF16 && (!a.has_bias || a.bdt == QK_BF16);
-  const bool fast = sb16 && std::is_same<XT, bf16>::value;
   const int mt = !fast ? 4 : a.m <= 1 ? 1 : a.m <= 2 ? 2 : 4;
-  if constexpr (PACK == QK_PACK_U8 || PACK == QK_PACK_S8_SYM) {
-    if (fast && a.m == 1 && LaunchM1I8<PACK>(a, cus, stream, st)) return true;
-  }
   const size_t lds = static_cast<size_t>(mt) * cpr * (64 + 4);
   if (lds > 64 * 1024) return false;
   if (fast && a.m == 1 && ChunkTraits<PACK>::kInt4 && lds <= 64 * 1024 &&
