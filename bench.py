@@ -33,6 +33,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "metal-pjrt-plugin_amd"))
 
 HBM_PEAK_GBS = 8000.0
+F32_PEAK_TFLOPS = 157.3
 BF16_PEAK_TFLOPS = 2500.0  # dense MFMA
 QWEN3_8B = [(4096, 4096), (12288, 4096), (4096, 12288), (151936, 4096)]
 GROUP = 64
@@ -136,6 +137,25 @@ def secondary(torch, qkern, dev, gen):
                     "ms": round(ms, 4), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                     "kernel": plan.describe().split("kernel=")[-1]})
         del a, b, d
+    # f32 GEMM C = A @ B at 1024^3 (C1), MFMA f32 peak
+    n = 1024
+    a = torch.randn(n, n, device=dev, generator=gen)
+    b = torch.randn(n, n, device=dev, generator=gen)
+    d = torch.empty(n, n, device=dev)
+    L = qkern.blas
+    lay = lambda r, c: L.MatrixLayout("float32", r, c)
+    plan = L.BlasLt.get_matmul_plan(
+        L.GemmConfig(lay(n, n), lay(n, n), lay(n, n), lay(n, n)),
+        L.Epilogue.kDefault)
+    args = L.MemoryArgs(a, b, None, d)
+    plan.execute_on_stream(None, args)
+    ms = timed_launches(torch, lambda i: plan.execute_on_stream(None, args), 20)
+    tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+    out.append({"name": "f32 gemm 1024x1024x1024", "value": round(tf, 1),
+                "unit": "TFLOP/s", "ms": round(ms, 4),
+                "frac": round(tf / F32_PEAK_TFLOPS, 4),
+                "kernel": plan.describe().split("kernel=")[-1]})
+    del a, b, d
     # int4 batched rows (decode batch / prefill) at 12288 x 4096
     n, k = 12288, 4096
     sets = [make_int4(torch, dev, n, k, gen) for _ in range(8)]
