@@ -271,14 +271,16 @@ template <typename T, int BN>
 qk_status DispatchFast(const GemmArgs& g, int batch, bool ta, bool tb,
                        hipStream_t stream, const char* name) {
   dim3 grid(g.tiles_m * g.tiles_n, batch);
+  using BN_ = DenseFastB<T, BN, 64, 256, false>;  // B stored [K][N]
+  using BT_ = DenseFastB<T, BN, 64, 256, true>;   // B stored [N][K]
   if (!ta && !tb)
-    gemm_fast_kernel<T, BN, false, false><<<grid, 256, 0, stream>>>(g);
+    gemm_fast_kernel<T, BN, false, BN_><<<grid, 256, 0, stream>>>(g);
   else if (!ta && tb)
-    gemm_fast_kernel<T, BN, false, true><<<grid, 256, 0, stream>>>(g);
+    gemm_fast_kernel<T, BN, false, BT_><<<grid, 256, 0, stream>>>(g);
   else if (ta && !tb)
-    gemm_fast_kernel<T, BN, true, false><<<grid, 256, 0, stream>>>(g);
+    gemm_fast_kernel<T, BN, true, BN_><<<grid, 256, 0, stream>>>(g);
   else
-    gemm_fast_kernel<T, BN, true, true><<<grid, 256, 0, stream>>>(g);
+    gemm_fast_kernel<T, BN, true, BT_><<<grid, 256, 0, stream>>>(g);
   return PostLaunch(name);
 }
 

@@ -514,11 +514,31 @@ struct BufferLoader {
   }
 };
 
-template <typename T, int BN, bool TA, bool TB>
+// Dense B operand of the interior-tile kernel: buffer loads of the tile as
+// stored (K-contiguous when KCONT), copied to LDS unchanged.
+template <typename T, int BN, int BK, int NT, bool KCONT>
+struct DenseFastB {
+  static constexpr bool kKCont = KCONT;
+  using Loader = BufferLoader<T, BN, BK, NT, KCONT>;
+  static constexpr int NV = Loader::NV;  // LDS stores per tile
+  Loader ld;
+  __device__ __forceinline__ DenseFastB(const GemmArgs& g, long long batch,
+                                        int tid) {
+    ld.init(static_cast<const T*>(g.b) + batch * g.bsb,
+            static_cast<long long>(KCONT ? g.n : g.k) * g.ldb * sizeof(T),
+            g.ldb, tid);
+  }
+  __device__ __forceinline__ void load(int n0, int k0) { ld.load(n0, k0); }
+  __device__ __forceinline__ void store(T* lds, int tid) const {
+    ld.store(lds, tid);
+  }
+};
+
+template <typename T, int BN, bool TA, class BSrc>
 __global__ __launch_bounds__(256) void gemm_fast_kernel(GemmArgs g) {
   constexpr int BM = 256, BK = 64, NT = 256, WM = 2, WN = 2;
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
-  constexpr bool AK = !TA, BKC = TB;  // K-contiguous operands
+  constexpr bool AK = !TA, BKC = BSrc::kKCont;  // K-contiguous operands
   using LA = TileLayout<T, BM, BK, AK>;
   using LB = TileLayout<T, BN, BK, BKC>;
   constexpr int kTileBytes = 2 * (LA::kElems + LB::kElems) * sizeof(T);
@@ -543,13 +563,10 @@ __global__ __launch_bounds__(256) void gemm_fast_kernel(GemmArgs g) {
   const long long batch = blockIdx.y;
 
   BufferLoader<T, BM, BK, NT, AK> la;
-  BufferLoader<T, BN, BK, NT, BKC> lb;
   la.init(static_cast<const T*>(g.a) + batch * g.bsa,
           static_cast<long long>(AK ? g.m : g.k) * g.lda * sizeof(T), g.lda,
           tid);
-  lb.init(static_cast<const T*>(g.b) + batch * g.bsb,
-          static_cast<long long>(BKC ? g.n : g.k) * g.ldb * sizeof(T), g.ldb,
-          tid);
+  BSrc lb(g, batch, tid);
 
   f32x16 acc[FM][FN];
 #pragma unroll
@@ -616,7 +633,7 @@ __global__ __launch_bounds__(256) void gemm_fast_kernel(GemmArgs g) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         if (s + 1 < BK / 16 && q < kReads)
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        if (s + 1 == BK / 16 && q < la.NV + lb.NV)
+        if (s + 1 == BK / 16 && q < la.NV + BSrc::NV)
           __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
       }
     }

@@ -162,6 +162,113 @@ struct QuantB {
   }
 };
 
+// Quantized B operand of the interior-tile kernel (gemm_common.h): weight
+// rows n0 .. n0 + BN of a K tile of 64 = one group of 64. Each thread
+// buffer-loads its part of one row's codes (16-byte loads, every row's
+// bytes contiguous across its TPR threads) and the group's bf16 scale and
+// offset, and writes T(f32(q) * f32(s) + f32(b)) (the unfused canonical
+// rounding of qk$dequantize) K-contiguously into LDS.
+template <int PACK, typename T, int BN>
+struct QuantFastB {
+  static constexpr bool kKCont = true;
+  static constexpr bool kInt4 = PACK == QK_PACK_U32X8;
+  static constexpr int NT = 256, BK = 64;
+  static constexpr int TPR = NT / BN;                // threads per row
+  static constexpr int KPT = BK / TPR;               // codes per thread
+  static constexpr int NL = (kInt4 ? KPT / 2 : KPT) / 16;  // 16 B loads
+  static constexpr int NV = KPT * static_cast<int>(sizeof(T)) / 16;
+  static constexpr int LD = TileLayout<T, BN, BK, true>::kLd;
+  static_assert(NL >= 1 && NV >= 1, "tile split");
+  __amdgpu_buffer_rsrc_t crs, srs, brs;
+  int row_bytes, G, r, kk0, cvo, svo;
+  u32x4 c[NL];
+  uint16_t sraw, braw;
+
+  __device__ __forceinline__ QuantFastB(const GemmArgs& g, long long /*b*/,
+                                        int tid)
+      : row_bytes(g.qrow_bytes), G(g.k / 64), r(tid / TPR),
+        kk0((tid % TPR) * KPT) {
+    crs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(g.b), (short)0,
+                                            g.n * row_bytes, 0x00020000);
+    srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(g.qscale),
+                                            (short)0, g.n * G * 2, 0x00020000);
+    brs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(g.qbias), (short)0, g.qhas_bias ? g.n * G * 2 : 0,
+        0x00020000);
+    cvo = r * row_bytes + (kInt4 ? kk0 / 2 : kk0);
+    svo = r * G * 2;
+  }
+  __device__ __forceinline__ void load(int n0, int k0) {
+    const int so = n0 * row_bytes + (kInt4 ? k0 / 2 : k0);
+#pragma unroll
+    for (int i = 0; i < NL; ++i)
+      c[i] = __builtin_amdgcn_raw_buffer_load_b128(crs, cvo + 16 * i, so, 2);
+    const int sg = n0 * G * 2 + (k0 / 64) * 2;
+    sraw = __builtin_amdgcn_raw_buffer_load_b16(srs, svo, sg, 0);
+    braw = __builtin_amdgcn_raw_buffer_load_b16(brs, svo, sg, 0);  // 0: none
+  }
+  __device__ __forceinline__ void store(T* lds, int /*tid*/) const {
+    const float sc = __uint_as_float(static_cast<uint32_t>(sraw) << 16);
+    const float bi = __uint_as_float(static_cast<uint32_t>(braw) << 16);
+    T* dst = lds + r * LD + kk0;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      union {
+        u32x4 u;
+        T e[8];
+      } o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = 8 * v + j;  // code index within the thread's run
+        float q;
+        if constexpr (kInt4) {
+          const uint32_t word = c[e / 32][(e % 32) / 8];
+          q = static_cast<float>((word >> (4 * (e % 8))) & 15u);
+        } else {
+          const uint32_t word = c[e / 16][(e % 16) / 4] >> (8 * (e % 4));
+          q = PACK == QK_PACK_S8_SYM
+                  ? static_cast<float>(static_cast<int8_t>(word & 255u))
+                  : static_cast<float>(word & 255u);
+        }
+        o.e[j] = from_f32<T>(__fadd_rn(__fmul_rn(q, sc), bi));
+      }
+      *reinterpret_cast<u32x4*>(dst + 8 * v) = o.u;
+    }
+  }
+};
+
+// The interior-tile kernel for M a multiple of 256, N of 128, group 64,
+// bf16 scales/offsets; false when it does not apply.
+template <typename T, int PACK>
+bool LaunchFastQ(GemmArgs g, int m, int n, hipStream_t stream,
+                 qk_status* st) {
+  if constexpr (PACK == QK_PACK_BYTE_HALFSPLIT) {
+    return false;
+  } else {
+    if (m % 256 != 0 || n % 128 != 0 || g.k % 64 != 0 || g.k == 0 ||
+        g.qgroup != 64 || g.qsdt != QK_BF16 ||
+        (g.qhas_bias && g.qbdt != QK_BF16) ||
+        static_cast<int64_t>(n) * g.qrow_bytes >= (int64_t{1} << 31) ||
+        static_cast<int64_t>(m) * g.k * 2 >= (int64_t{1} << 31) ||
+        reinterpret_cast<uintptr_t>(g.a) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(g.b) % 16 != 0)
+      return false;
+    const int cus = DeviceComputeUnits();
+    const bool wide = n % 256 == 0 && (m / 256) * (n / 256) >= cus;
+    g.tiles_m = m / 256;
+    g.tiles_n = n / (wide ? 256 : 128);
+    const dim3 grid(g.tiles_m * g.tiles_n);
+    if (wide)
+      gemm_fast_kernel<T, 256, false, QuantFastB<PACK, T, 256>>
+          <<<grid, 256, 0, stream>>>(g);
+    else
+      gemm_fast_kernel<T, 128, false, QuantFastB<PACK, T, 128>>
+          <<<grid, 256, 0, stream>>>(g);
+    *st = PostLaunch("qgemm_fast");
+    return true;
+  }
+}
+
 template <typename T, int PACK, int BM, int BN, int WM, int WN>
 qk_status LaunchTileQ(const GemmArgs& g, hipStream_t stream) {
   constexpr int NT = WM * WN * 64;
@@ -173,6 +280,8 @@ qk_status LaunchTileQ(const GemmArgs& g, hipStream_t stream) {
 
 template <typename T, int PACK>
 qk_status LaunchQ(const GemmArgs& g0, int m, int n, hipStream_t stream) {
+  qk_status st = QK_OK;
+  if (LaunchFastQ<T, PACK>(g0, m, n, stream, &st)) return st;
   GemmArgs g = g0;
   const int cus = DeviceComputeUnits();
   auto ceil_div = [](long long a, long long b) { return (a + b - 1) / b; };

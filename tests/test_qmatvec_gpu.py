@@ -144,6 +144,35 @@ def test_qmatvec_few_rows(dev, mnk, packing):
         check_matvec(y.float().cpu().numpy().astype(np.float64), x, w)
 
 
+@pytest.mark.parametrize("case", [
+    (256, 384, 1024, Packing.U32X8, "bfloat16"),
+    (512, 1024, 2048, Packing.U8, "bfloat16"),
+    (256, 512, 1024, Packing.S8_SYM, "bfloat16"),
+    (256, 256, 512, Packing.U32X8, "float16"),
+    (2048, 8192, 256, Packing.U32X8, "bfloat16"),  # 256-column tiles
+])
+def test_qmatvec_prefill_tiles(dev, case):
+    """Row counts that are multiples of 256 (the interior-tile GEMM with
+    the dequantizing B loader), each packing it takes, bf16 and f16 x,
+    with and without offsets. Like the reference's linear() for more than
+    four rows (examples/llm/qwen3.py:215-230), the weights are dequantized
+    to x's type first, so the float64 oracle multiplies by those rounded
+    weights."""
+    m, n, k, packing, xdt = case
+    rng = np.random.default_rng(m + n + k)
+    for has_bias in (True, False):
+        dc, ds, db, w, *_ = make_weights(rng, n, k, packing, 64,
+                                         has_bias=has_bias)
+        x = O.round_to(rng.standard_normal((m, k)), xdt).astype(np.float32)
+        y = qkern.qmatvec(torch.from_numpy(x).to(TORCH[xdt]).to(dev),
+                          dc.to(dev), ds.to(dev),
+                          None if db is None else db.to(dev),
+                          packing=packing)
+        torch.cuda.synchronize()
+        check_matvec(y.float().cpu().numpy().astype(np.float64), x,
+                     O.round_to(w, xdt))
+
+
 def test_qmatvec_leading_dims_and_no_bias(dev):
     rng = np.random.default_rng(5)
     dc, ds, _, w, *_ = make_weights(rng, 40, 256, Packing.U32X8, 64,
