@@ -284,6 +284,24 @@ qk_status DispatchFast(const GemmArgs& g, int batch, bool ta, bool tb,
   return PostLaunch(name);
 }
 
+template <typename T, int BMN, int KW>
+qk_status DispatchSplitK(const GemmArgs& g, int batch, bool ta, bool tb,
+                         hipStream_t stream, const char* name) {
+  dim3 grid(g.tiles_m * g.tiles_n, batch);
+  using BN_ = DenseB<T, BMN, 64, 64, false>;
+  using BT_ = DenseB<T, BMN, 64, 64, true>;
+  constexpr int NT = KW * 64;
+  if (!ta && !tb)
+    gemm_splitk_kernel<T, BMN, BMN, 64, KW, false, BN_><<<grid, NT, 0, stream>>>(g);
+  else if (!ta && tb)
+    gemm_splitk_kernel<T, BMN, BMN, 64, KW, false, BT_><<<grid, NT, 0, stream>>>(g);
+  else if (ta && !tb)
+    gemm_splitk_kernel<T, BMN, BMN, 64, KW, true, BN_><<<grid, NT, 0, stream>>>(g);
+  else
+    gemm_splitk_kernel<T, BMN, BMN, 64, KW, true, BT_><<<grid, NT, 0, stream>>>(g);
+  return PostLaunch(name);
+}
+
 struct TileCfg {
   int bm, bn, bk, wm, wn;
 };
@@ -325,8 +343,10 @@ constexpr HalfTile kHalfTiles[] = {
     {128, 256, 2, 2},  // 5
     {256, 256, 2, 2},  // 6: interior-tile kernel (gemm_fast_kernel)
     {256, 128, 2, 2},  // 7: interior-tile kernel, 128 x 64 per wave
+    {64, 64, 2, 2},    // 8: split-K, four waves each a quarter of K
+    {32, 32, 2, 4},    // 9: split-K for up to 32 rows, eight waves
 };
-constexpr int kFastTile256 = 6, kFastTile128 = 7;
+constexpr int kFastTile256 = 6, kFastTile128 = 7, kSplitK = 8, kSplitK32 = 9;
 constexpr int kNumHalfTiles = sizeof(kHalfTiles) / sizeof(kHalfTiles[0]);
 
 // QK_GEMM_TILE=<index into kHalfTiles> forces a configuration (tuning).
@@ -380,6 +400,10 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
           0.67 * static_cast<double>(CeilDiv(tiles(256, 128), cus));
       t = FastApplies(p, 256) && r256 <= r128 ? kFastTile256 : kFastTile128;
     }
+    // Few 64x64 tiles and a long K: split K over the waves of each tile
+    // (32x32 tiles and eight waves for at most 32 rows or columns).
+    if (t < 0 && tiles(64, 64) < 2 * cus && CeilDiv(p.k, 64) >= 16)
+      t = std::min(p.m, p.n) <= 32 ? kSplitK32 : kSplitK;
     if (t < 0) {
       // Rounds of resident tiles on the 256 CUs: one 256x256 tile (8
       // waves) per CU, two 128x128 tiles per CU. Measured on MI355X, a
@@ -401,8 +425,13 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
       c.bm = 64, c.bn = 64, c.bk = 32;
     }
   }
-  const bool fast = half && c.tile >= kFastTile256;
-  c.name = std::string(!half ? "gemm_mfma_" : fast ? "gemm_fast_" : "gemm_tile_") +
+  const bool fast = half && (c.tile == kFastTile256 || c.tile == kFastTile128);
+  const bool splitk = half && (c.tile == kSplitK || c.tile == kSplitK32);
+  c.name = std::string(!half      ? "gemm_mfma_"
+                       : fast     ? "gemm_fast_"
+                       : splitk   ? (c.tile == kSplitK ? "gemm_splitk4_"
+                                                           : "gemm_splitk8_")
+                                  : "gemm_tile_") +
            DTypeName(p.a.dtype) + "_" + std::to_string(c.bm) + "x" +
            std::to_string(c.bn) + "x" + std::to_string(c.bk) +
            (half ? "_w" + std::to_string(kHalfTiles[c.tile].wm *
@@ -430,6 +459,10 @@ qk_status DispatchHalf(int tile, const GemmArgs& g, int batch, bool ta,
       return DispatchFast<T, 256>(g, batch, ta, tb, st, name);
     case kFastTile128:
       return DispatchFast<T, 128>(g, batch, ta, tb, st, name);
+    case kSplitK:
+      return DispatchSplitK<T, 64, 4>(g, batch, ta, tb, st, name);
+    case kSplitK32:
+      return DispatchSplitK<T, 32, 8>(g, batch, ta, tb, st, name);
     default:
       return DispatchTile<T, 64, 64, 64, 2, 2>(g, batch, ta, tb, st, name);
   }

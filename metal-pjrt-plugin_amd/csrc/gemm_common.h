@@ -654,5 +654,130 @@ __global__ __launch_bounds__(256) void gemm_fast_kernel(GemmArgs g) {
 }
 
 
+
+// ---------------------------------------------------------------------------
+// Split-K tile kernel for problems with few output tiles and long K (skinny
+// GEMMs, quantized matmuls of 65..255 rows): the KW waves of a workgroup
+// each walk a contiguous quarter (for KW = 4) of the K tiles of the same
+// BM x BN output tile, through a wave-private LDS stage (a wave's LDS
+// operations run in order, so no workgroup barrier is needed in the K
+// loop; the next K tile is loaded into registers while the current one is
+// used). The KW partial tiles are summed through LDS and the epilogue
+// (alpha, beta C, bias, aux, activation) is applied once. BSrc is a B
+// loader of the tiled kernel built for 64 threads (one wave).
+template <typename T, int BM, int BN, int BK, int KW, bool TA, class BSrc>
+__global__ __launch_bounds__(KW * 64) void gemm_splitk_kernel(GemmArgs g) {
+  constexpr int NT = KW * 64;
+  constexpr int FM = BM / 32, FN = BN / 32;
+  constexpr bool AK = !TA, BKC = BSrc::kKCont;
+  using LA = TileLayout<T, BM, BK, AK>;
+  using LB = TileLayout<T, BN, BK, BKC>;
+  constexpr int kWaveBytes = (LA::kElems + LB::kElems) * sizeof(T);
+  constexpr int kLdo = BN + 4;
+  constexpr int kSumBytes = KW * BM * kLdo * 4;
+  __shared__ __attribute__((aligned(16)))
+  unsigned char lds_raw[KW * kWaveBytes > kSumBytes ? KW * kWaveBytes
+                                                    : kSumBytes];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  T* const lds_a = reinterpret_cast<T*>(lds_raw + wave * kWaveBytes);
+  T* const lds_b = lds_a + LA::kElems;
+
+  const int nwg = g.tiles_m * g.tiles_n;
+  int bid = blockIdx.x;
+  if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+  const int tm = bid % g.tiles_m, tn = bid / g.tiles_m;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const long long batch = blockIdx.y;
+  const T* A = static_cast<const T*>(g.a) + batch * g.bsa;
+
+  DirectLoader<T, BM, BK, 64, AK> la;
+  BSrc lb(g, batch, n0, lane);
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int ktiles = (g.k + BK - 1) / BK;
+  const int kb = wave * ktiles / KW, ke = (wave + 1) * ktiles / KW;
+  if (kb < ke) {
+    la.load(A, g.lda, m0, kb * BK, g.m, g.k, g.a_vec, lane);
+    lb.load(kb * BK);
+  }
+  for (int kt = kb; kt < ke; ++kt) {
+    la.store(lds_a, lane);
+    lb.store(lds_b);
+    if (kt + 1 < ke) {
+      la.load(A, g.lda, m0, (kt + 1) * BK, g.m, g.k, g.a_vec, lane);
+      lb.load((kt + 1) * BK);
+    }
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      typename Frag<T>::type fa[FM], fb[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        fa[i] = load_frag<T, BM, BK, AK>(lds_a, i * 32, ks * 16, lane);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        fb[j] = load_frag<T, BN, BK, BKC>(lds_b, j * 32, ks * 16, lane);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) mma(acc[i][j], fa[i], fb[j]);
+    }
+  }
+
+  // Sum the KW partial tiles: wave w writes its tile to slice w, then all
+  // threads add the slices for four consecutive columns and store them
+  // with the epilogue.
+  __syncthreads();
+  float* sum = reinterpret_cast<float*>(lds_raw);
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int col = j * 32 + (lane & 31);
+        sum[(wave * BM + row) * kLdo + col] = acc[i][j][r];
+      }
+  __syncthreads();
+  const bool of32 = g.out_f32 != 0;
+  const bool vec = g.out_vec != 0;
+  const long long dbase = batch * g.bsd;
+  for (int q = tid; q < BM * BN / 4; q += NT) {
+    const int lr = q / (BN / 4), lc = (q % (BN / 4)) * 4;
+    const int row = m0 + lr, col = n0 + lc;
+    if (row >= g.m || col >= g.n) continue;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < KW; ++w) {
+      const float4 p =
+          *reinterpret_cast<const float4*>(sum + (w * BM + lr) * kLdo + lc);
+      v[0] += p.x, v[1] += p.y, v[2] += p.z, v[3] += p.w;
+    }
+    const int cnt = min(4, g.n - col);
+    const long long idx = dbase + static_cast<long long>(row) * g.ldd + col;
+    float c4[4] = {0.f, 0.f, 0.f, 0.f}, b4[4] = {0.f, 0.f, 0.f, 0.f};
+    if (g.use_c) ld_out4<T>(g.c, idx, of32, vec, cnt, c4);
+    if (g.has_bias) ld_out4<T>(g.bias, col, of32, false, cnt, b4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = g.alpha * v[e];
+      if (g.use_c) v[e] += g.beta * c4[e];
+      if (g.has_bias) v[e] += b4[e];
+    }
+    if (g.has_aux) st_out4<T>(g.aux, idx, of32, vec, cnt, v);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = act_f32(g.act, v[e]);
+    st_out4<T>(g.d, idx, of32, vec, cnt, v);
+  }
+}
+
 }  // namespace
 }  // namespace qk

@@ -303,6 +303,13 @@ qk_status LaunchQ(const GemmArgs& g0, int m, int n, hipStream_t stream) {
   }
   if (cfg == 1) return LaunchTileQ<T, PACK, 256, 256, 2, 4>(g, stream);
   if (cfg == 2) return LaunchTileQ<T, PACK, 128, 128, 2, 2>(g, stream);
+  if (g.k / 64 >= 16) {
+    // Few 64x64 tiles and a long K: four waves per tile, each a quarter of
+    // the K tiles, reduced through LDS.
+    gemm_splitk_kernel<T, 64, 64, 64, 4, false, QuantB<PACK, T, 64, 64, 64>>
+        <<<dim3(g.tiles_m * g.tiles_n), 256, 0, stream>>>(g);
+    return PostLaunch("qgemm_splitk");
+  }
   return LaunchTileQ<T, PACK, 64, 64, 2, 2>(g, stream);
 }
 

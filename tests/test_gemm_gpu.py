@@ -243,6 +243,38 @@ def test_activation_special_values(dev, epilogue):
         assert ok.all(), list(zip(vals[~ok], row[~ok], want[~ok]))
 
 
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_split_k_kernel(dev, ta, tb):
+    """Few output tiles and a long K run the split-K kernel (each wave a
+    quarter of K, reduced through LDS): ragged M/N/K, all transposes."""
+    plan = run_case(dev, 64, 512, 2048, ta=ta, tb=tb)
+    assert "gemm_splitk4" in plan.describe()
+    plan = run_case(dev, 100, 260, 1500, ta=ta, tb=tb, tin="float16",
+                    beta=0.5)
+    assert "gemm_splitk4" in plan.describe()
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_split_k_kernel_few_rows(dev, ta, tb):
+    """At most 32 rows (or columns): 32x32 tiles, eight waves over K."""
+    plan = run_case(dev, 16, 700, 2048, ta=ta, tb=tb)
+    assert "gemm_splitk8" in plan.describe()
+    plan = run_case(dev, 300, 5, 1100, ta=ta, tb=tb, tin="float16",
+                    epilogue=Epilogue.kBiasThenSILU)
+    assert "gemm_splitk8" in plan.describe()
+
+
+def test_split_k_kernel_epilogues(dev):
+    plan = run_case(dev, 32, 1000, 4096, epilogue=Epilogue.kBiasThenSILUWithAux,
+                    separate_c=True, beta=1.0)
+    assert "gemm_splitk8" in plan.describe()
+    plan = run_case(dev, 48, 384, 1024, batch=3, pad=8, tout="float32",
+                    epilogue=Epilogue.kBiasThenGELU)
+    assert "gemm_splitk4" in plan.describe()
+
+
 def test_large_k(dev):
     run_case(dev, 64, 64, 4096, tout="float32")
     run_case(dev, 64, 64, 4096, tin="float32")
