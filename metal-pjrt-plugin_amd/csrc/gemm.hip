@@ -288,17 +288,19 @@ template <typename T, int BMN, int KW>
 qk_status DispatchSplitK(const GemmArgs& g, int batch, bool ta, bool tb,
                          hipStream_t stream, const char* name) {
   dim3 grid(g.tiles_m * g.tiles_n, batch);
+  using AN = DenseA<T, BMN, 64, 64, true>;   // A stored [M][K]
+  using AT = DenseA<T, BMN, 64, 64, false>;  // A stored [K][M]
   using BN_ = DenseB<T, BMN, 64, 64, false>;
   using BT_ = DenseB<T, BMN, 64, 64, true>;
   constexpr int NT = KW * 64;
   if (!ta && !tb)
-    gemm_splitk_kernel<T, BMN, BMN, 64, KW, false, BN_><<<grid, NT, 0, stream>>>(g);
+    gemm_splitk_kernel<T, BMN, BMN, 64, KW, AN, BN_><<<grid, NT, 0, stream>>>(g);
   else if (!ta && tb)
-    gemm_splitk_kernel<T, BMN, BMN, 64, KW, false, BT_><<<grid, NT, 0, stream>>>(g);
+    gemm_splitk_kernel<T, BMN, BMN, 64, KW, AN, BT_><<<grid, NT, 0, stream>>>(g);
   else if (ta && !tb)
-    gemm_splitk_kernel<T, BMN, BMN, 64, KW, true, BN_><<<grid, NT, 0, stream>>>(g);
+    gemm_splitk_kernel<T, BMN, BMN, 64, KW, AT, BN_><<<grid, NT, 0, stream>>>(g);
   else
-    gemm_splitk_kernel<T, BMN, BMN, 64, KW, true, BT_><<<grid, NT, 0, stream>>>(g);
+    gemm_splitk_kernel<T, BMN, BMN, 64, KW, AT, BT_><<<grid, NT, 0, stream>>>(g);
   return PostLaunch(name);
 }
 
@@ -419,6 +421,7 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
     c.tile = t;
     c.bm = kHalfTiles[t].bm, c.bn = kHalfTiles[t].bn, c.bk = 64;
   } else {
+    c.tile = -1;
     if (tiles(128, 128) >= 192) {
       c.bm = 128, c.bn = 128, c.bk = 32;
     } else {
@@ -426,17 +429,17 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
     }
   }
   const bool fast = half && (c.tile == kFastTile256 || c.tile == kFastTile128);
-  const bool splitk = half && (c.tile == kSplitK || c.tile == kSplitK32);
-  c.name = std::string(!half      ? "gemm_mfma_"
+  const bool splitk = c.tile == kSplitK || c.tile == kSplitK32;
+  c.name = std::string(splitk     ? (c.tile == kSplitK ? "gemm_splitk4_"
+                                                       : "gemm_splitk8_")
+                       : !half    ? "gemm_mfma_"
                        : fast     ? "gemm_fast_"
-                       : splitk   ? (c.tile == kSplitK ? "gemm_splitk4_"
-                                                           : "gemm_splitk8_")
                                   : "gemm_tile_") +
            DTypeName(p.a.dtype) + "_" + std::to_string(c.bm) + "x" +
            std::to_string(c.bn) + "x" + std::to_string(c.bk) +
-           (half ? "_w" + std::to_string(kHalfTiles[c.tile].wm *
-                                         kHalfTiles[c.tile].wn)
-                 : std::string()) +
+           (c.tile >= 0 ? "_w" + std::to_string(kHalfTiles[c.tile].wm *
+                                                kHalfTiles[c.tile].wn)
+                        : std::string()) +
            (p.a.transpose ? "_t" : "_n") + (p.b.transpose ? "t" : "n");
   return c;
 }

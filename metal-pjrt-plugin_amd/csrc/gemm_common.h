@@ -665,11 +665,34 @@ __global__ __launch_bounds__(256) void gemm_fast_kernel(GemmArgs g) {
 // used). The KW partial tiles are summed through LDS and the epilogue
 // (alpha, beta C, bias, aux, activation) is applied once. BSrc is a B
 // loader of the tiled kernel built for 64 threads (one wave).
-template <typename T, int BM, int BN, int BK, int KW, bool TA, class BSrc>
+// A operand loaded as stored (AK: K-contiguous), for the split-K kernel.
+template <typename T, int BM, int BK, int NT, bool AK>
+struct DenseA {
+  static constexpr bool kKCont = AK;
+  DirectLoader<T, BM, BK, NT, AK> ld;
+  const T* src;
+  int lda, m0, m, k, tid;
+  bool vec;
+  __device__ __forceinline__ DenseA(const GemmArgs& g, long long batch,
+                                    int m0_, int tid_)
+      : src(static_cast<const T*>(g.a) + batch * g.bsa),
+        lda(g.lda),
+        m0(m0_),
+        m(g.m),
+        k(g.k),
+        tid(tid_),
+        vec(g.a_vec != 0) {}
+  __device__ __forceinline__ void load(int k0) {
+    ld.load(src, lda, m0, k0, m, k, vec, tid);
+  }
+  __device__ __forceinline__ void store(T* lds) const { ld.store(lds, tid); }
+};
+
+template <typename T, int BM, int BN, int BK, int KW, class ASrc, class BSrc>
 __global__ __launch_bounds__(KW * 64) void gemm_splitk_kernel(GemmArgs g) {
   constexpr int NT = KW * 64;
   constexpr int FM = BM / 32, FN = BN / 32;
-  constexpr bool AK = !TA, BKC = BSrc::kKCont;
+  constexpr bool AK = ASrc::kKCont, BKC = BSrc::kKCont;
   using LA = TileLayout<T, BM, BK, AK>;
   using LB = TileLayout<T, BN, BK, BKC>;
   constexpr int kWaveBytes = (LA::kElems + LB::kElems) * sizeof(T);
@@ -689,9 +712,7 @@ __global__ __launch_bounds__(KW * 64) void gemm_splitk_kernel(GemmArgs g) {
   const int tm = bid % g.tiles_m, tn = bid / g.tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
   const long long batch = blockIdx.y;
-  const T* A = static_cast<const T*>(g.a) + batch * g.bsa;
-
-  DirectLoader<T, BM, BK, 64, AK> la;
+  ASrc la(g, batch, m0, lane);
   BSrc lb(g, batch, n0, lane);
 
   f32x16 acc[FM][FN];
@@ -705,14 +726,14 @@ __global__ __launch_bounds__(KW * 64) void gemm_splitk_kernel(GemmArgs g) {
   const int ktiles = (g.k + BK - 1) / BK;
   const int kb = wave * ktiles / KW, ke = (wave + 1) * ktiles / KW;
   if (kb < ke) {
-    la.load(A, g.lda, m0, kb * BK, g.m, g.k, g.a_vec, lane);
+    la.load(kb * BK);
     lb.load(kb * BK);
   }
   for (int kt = kb; kt < ke; ++kt) {
-    la.store(lds_a, lane);
+    la.store(lds_a);
     lb.store(lds_b);
     if (kt + 1 < ke) {
-      la.load(A, g.lda, m0, (kt + 1) * BK, g.m, g.k, g.a_vec, lane);
+      la.load((kt + 1) * BK);
       lb.load((kt + 1) * BK);
     }
 #pragma unroll

@@ -306,7 +306,8 @@ qk_status LaunchQ(const GemmArgs& g0, int m, int n, hipStream_t stream) {
   if (g.k / 64 >= 16) {
     // Few 64x64 tiles and a long K: four waves per tile, each a quarter of
     // the K tiles, reduced through LDS.
-    gemm_splitk_kernel<T, 64, 64, 64, 4, false, QuantB<PACK, T, 64, 64, 64>>
+    gemm_splitk_kernel<T, 64, 64, 64, 4, DenseA<T, 64, 64, 64, true>,
+                       QuantB<PACK, T, 64, 64, 64>>
         <<<dim3(g.tiles_m * g.tiles_n), 256, 0, stream>>>(g);
     return PostLaunch("qgemm_splitk");
   }

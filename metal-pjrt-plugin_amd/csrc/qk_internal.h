@@ -64,7 +64,7 @@ struct GemmProblem {
 struct GemmKernelChoice {
   int family = 0;  // 0 MFMA tiles, 1 skinny (few rows / columns)
   int bm = 0, bn = 0, bk = 0;
-  int tile = 0;  // f16/bf16 tile configuration index
+  int tile = 0;  // tile configuration index (gemm.hip); -1: the f32 tiles
   int split_k = 1;
   std::string name;
 };
