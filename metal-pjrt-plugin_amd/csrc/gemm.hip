@@ -20,6 +20,10 @@
 //  - Workgroup ids are remapped so that consecutive tiles share an XCD
 //    (the hardware deals workgroups round-robin over the 8 XCDs, each with
 //    its own L2) and tiles are visited in groups of GROUP_M tile rows.
+//  - Problems that are whole multiples of 256 x BN x 64 with 16-byte
+//    aligned operands take gemm_dma_kernel (gemm_dma.h): operand tiles go
+//    from global memory straight into XOR-swizzled LDS stages, and the
+//    epilogue is applied from the accumulators without LDS staging.
 
 #include <hip/hip_runtime.h>
 
@@ -29,6 +33,7 @@
 #include <string>
 
 #include "gemm_common.h"
+#include "gemm_dma.h"
 #include "qk_device.h"
 #include "qk_internal.h"
 
@@ -271,16 +276,14 @@ template <typename T, int BN>
 qk_status DispatchFast(const GemmArgs& g, int batch, bool ta, bool tb,
                        hipStream_t stream, const char* name) {
   dim3 grid(g.tiles_m * g.tiles_n, batch);
-  using BN_ = DenseFastB<T, BN, 64, 256, false>;  // B stored [K][N]
-  using BT_ = DenseFastB<T, BN, 64, 256, true>;   // B stored [N][K]
   if (!ta && !tb)
-    gemm_fast_kernel<T, BN, false, BN_><<<grid, 256, 0, stream>>>(g);
+    gemm_dma_kernel<T, BN, false, false><<<grid, 256, 0, stream>>>(g);
   else if (!ta && tb)
-    gemm_fast_kernel<T, BN, false, BT_><<<grid, 256, 0, stream>>>(g);
+    gemm_dma_kernel<T, BN, false, true><<<grid, 256, 0, stream>>>(g);
   else if (ta && !tb)
-    gemm_fast_kernel<T, BN, true, BN_><<<grid, 256, 0, stream>>>(g);
+    gemm_dma_kernel<T, BN, true, false><<<grid, 256, 0, stream>>>(g);
   else
-    gemm_fast_kernel<T, BN, true, BT_><<<grid, 256, 0, stream>>>(g);
+    gemm_dma_kernel<T, BN, true, true><<<grid, 256, 0, stream>>>(g);
   return PostLaunch(name);
 }
 
@@ -343,8 +346,8 @@ constexpr HalfTile kHalfTiles[] = {
     {64, 64, 2, 2},    // 3
     {256, 128, 2, 2},  // 4
     {128, 256, 2, 2},  // 5
-    {256, 256, 2, 2},  // 6: interior-tile kernel (gemm_fast_kernel)
-    {256, 128, 2, 2},  // 7: interior-tile kernel, 128 x 64 per wave
+    {256, 256, 2, 2},  // 6: interior-tile LDS-DMA kernel (gemm_dma_kernel)
+    {256, 128, 2, 2},  // 7: interior-tile LDS-DMA kernel, 128 x 64 per wave
     {64, 64, 2, 2},    // 8: split-K, four waves each a quarter of K
     {32, 32, 2, 4},    // 9: split-K for up to 32 rows, eight waves
 };

@@ -458,9 +458,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs g) {
 
 
 // ---------------------------------------------------------------------------
-// Interior-tile f16/bf16 kernel for problems whose M, N and K are multiples
-// of the tile (BM = 256, BN = 256 or 128, BK = 64) and whose operands allow
-// 16-byte loads: no bounds checks in the K loop.
+// Interior-tile f16/bf16 kernel with a register-staged B source (used by
+// the quantized matmul, whose B tile is dequantized on its way into LDS;
+// dense operands take the LDS-DMA kernel of gemm_dma.h) for problems whose
+// M, N and K are multiples of the tile (BM = 256, BN = 256 or 128,
+// BK = 64) and whose operands allow 16-byte loads: no bounds checks in the
+// K loop.
 //
 //  - Four waves (2 x 2), each owning a 128 x BN/2 block of D: 16 (or 8)
 //    32x32 accumulators, so one wave per SIMD keeps every MFMA pipe fed.
@@ -514,25 +517,88 @@ struct BufferLoader {
   }
 };
 
-// Dense B operand of the interior-tile kernel: buffer loads of the tile as
-// stored (K-contiguous when KCONT), copied to LDS unchanged.
-template <typename T, int BN, int BK, int NT, bool KCONT>
-struct DenseFastB {
-  static constexpr bool kKCont = KCONT;
-  using Loader = BufferLoader<T, BN, BK, NT, KCONT>;
-  static constexpr int NV = Loader::NV;  // LDS stores per tile
-  Loader ld;
-  __device__ __forceinline__ DenseFastB(const GemmArgs& g, long long batch,
-                                        int tid) {
-    ld.init(static_cast<const T*>(g.b) + batch * g.bsb,
-            static_cast<long long>(KCONT ? g.n : g.k) * g.ldb * sizeof(T),
-            g.ldb, tid);
+
+// Epilogue straight from the accumulators, for tiles wholly inside D (no
+// bounds checks): the lane holding element (row, col) of a 32x32 block
+// applies alpha, beta*C, bias, aux and the activation and stores it; the
+// 32 lanes of a half-wave write 32 consecutive columns of one row. The
+// output type and activation are template arguments, chosen once by
+// store_direct, so the per-element code has no branches on them.
+// Arithmetic order as store_tile: alpha*acc, + beta*C, + bias.
+template <typename O, int ACT, int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_direct_t(
+    const GemmArgs& g, const f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
+    int m0, int n0, long long batch, int lane, int wm, int wn) {
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  const long long dbase = batch * g.bsd;
+  const int colb = n0 + wn * WTN + (lane & 31);
+  const int rowb = m0 + wm * WTM + 4 * (lane >> 5);
+  float bias[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+    bias[j] = g.has_bias ? to_f32(static_cast<const O*>(g.bias)[colb + j * 32])
+                         : 0.f;
+  const O* C = static_cast<const O*>(g.c);
+  O* aux = static_cast<O*>(g.aux);
+  O* D = static_cast<O*>(g.d);
+  // One block row (i) at a time; each optional term is one uniform branch
+  // around a loop over the block row's FN x 16 values.
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    float v[FN][16];
+    long long rb[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      rb[r] = dbase + static_cast<long long>(rowb + i * 32 + 8 * (r >> 2) + (r & 3)) * g.ldd + colb;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[j][r] = g.alpha * acc[i][j][r];
+    if (g.use_c) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[j][r] += g.beta * to_f32(C[rb[r] + j * 32]);
+    }
+    if (g.has_bias) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[j][r] += bias[j];
+    }
+    if (g.has_aux) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) aux[rb[r] + j * 32] = from_f32<O>(v[j][r]);
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) D[rb[r] + j * 32] = from_f32<O>(act_f32(ACT, v[j][r]));
   }
-  __device__ __forceinline__ void load(int n0, int k0) { ld.load(n0, k0); }
-  __device__ __forceinline__ void store(T* lds, int tid) const {
-    ld.store(lds, tid);
-  }
-};
+}
+template <typename T, int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_direct(
+    const GemmArgs& g, const f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
+    int m0, int n0, long long batch, int lane, int wm, int wn) {
+  auto go = [&](auto out) {
+    using O = decltype(out);
+    switch (g.act) {
+      case 1:
+        return store_direct_t<O, 1, BM, BN, WM, WN>(g, acc, m0, n0, batch, lane, wm, wn);
+      case 2:
+        return store_direct_t<O, 2, BM, BN, WM, WN>(g, acc, m0, n0, batch, lane, wm, wn);
+      case 3:
+        return store_direct_t<O, 3, BM, BN, WM, WN>(g, acc, m0, n0, batch, lane, wm, wn);
+      default:
+        return store_direct_t<O, 0, BM, BN, WM, WN>(g, acc, m0, n0, batch, lane, wm, wn);
+    }
+  };
+  if (g.out_f32) go(0.f);
+  else go(T{});
+}
 
 template <typename T, int BN, bool TA, class BSrc>
 __global__ __launch_bounds__(256) void gemm_fast_kernel(GemmArgs g) {
@@ -542,9 +608,7 @@ __global__ __launch_bounds__(256) void gemm_fast_kernel(GemmArgs g) {
   using LA = TileLayout<T, BM, BK, AK>;
   using LB = TileLayout<T, BN, BK, BKC>;
   constexpr int kTileBytes = 2 * (LA::kElems + LB::kElems) * sizeof(T);
-  constexpr int kOutBytes = WTM * (BN + 4) * 4;
-  __shared__ __attribute__((aligned(16)))
-  unsigned char lds_raw[kTileBytes > kOutBytes ? kTileBytes : kOutBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kTileBytes];
   T* const base = reinterpret_cast<T*>(lds_raw);
   auto lds_a = [&](int s) { return base + s * LA::kElems; };
   auto lds_b = [&](int s) { return base + 2 * LA::kElems + s * LB::kElems; };
@@ -647,10 +711,7 @@ __global__ __launch_bounds__(256) void gemm_fast_kernel(GemmArgs g) {
       fb[0][j] = load_frag<T, BN, BK, BKC>(lds_b(cur ^ 1), wn * WTN + j * 32,
                                            0, lane);
   }
-  // The fragment reads after the last barrier touch the stage the epilogue
-  // overwrites first.
-  __syncthreads();
-  store_tile<T, BM, BN, WM, WN>(g, acc, lds_raw, m0, n0, batch, tid);
+  store_direct<T, BM, BN, WM, WN>(g, acc, m0, n0, batch, lane, wm, wn);
 }
 
 

@@ -186,6 +186,9 @@ def test_interior_tile_kernel(dev, ta, tb):
     plan = run_case(dev, 4096, 4096, 64, ta=ta, tb=tb, beta=1.0,
                     tin="float16")
     assert "gemm_fast_f16_256x256" in plan.describe()
+    # an odd number (5) of K tiles: the loop's unpaired last tile
+    plan = run_case(dev, 4096, 2048, 320, ta=ta, tb=tb)
+    assert "gemm_fast_bf16" in plan.describe()
 
 
 def test_interior_tile_kernel_epilogues(dev):
