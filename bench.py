@@ -132,10 +132,26 @@ def secondary(torch, qkern, dev, gen):
         ms = timed_launches(torch, lambda i: plan.execute_on_stream(None, args),
                             20)
         tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        # hipBLASLt (torch.matmul, no epilogue) on the same operands, for
+        # reference: eager launches between two events (kept out of graph
+        # capture, as library calls may record memsets)
+        for _ in range(3):
+            torch.matmul(a, b, out=d)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(20):
+            torch.matmul(a, b, out=d)
+        e1.record()
+        torch.cuda.synchronize()
+        ms_lt = e0.elapsed_time(e1) / 20
         out.append({"name": f"bf16 gemm+bias+silu {m}x{n}x{k}",
                     "value": round(tf, 1), "unit": "TFLOP/s",
                     "ms": round(ms, 4), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
-                    "kernel": plan.describe().split("kernel=")[-1]})
+                    "kernel": plan.describe().split("kernel=")[-1],
+                    "hipblaslt_matmul_tflops": round(
+                        2.0 * m * n * k / (ms_lt * 1e-3) / 1e12, 1)})
         del a, b, d
     # f32 GEMM C = A @ B at 1024^3 (C1), MFMA f32 peak
     n = 1024
