@@ -98,6 +98,11 @@ qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream);
 bool QSkinnyApplies(const QuantProblem& p);
 qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream);
 
+// Quantized matmul for up to 128 rows of x (qmid.hip): int4 u32x8 or
+// int8, bf16, group 64, K a multiple of 256.
+bool QMidApplies(const QuantProblem& p);
+qk_status LaunchQMid(const QuantProblem& p, hipStream_t stream);
+
 // Dequantizing MFMA GEMM (qgemm.hip) for more than four rows of x.
 bool QGemmApplies(const QuantProblem& p);
 qk_status LaunchQGemm(const QuantProblem& p, hipStream_t stream);

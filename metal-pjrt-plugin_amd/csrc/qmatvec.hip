@@ -1279,10 +1279,12 @@ qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream) {
   const int m = static_cast<int>(p.m);
   // Beyond four rows the reference's linear() (ROWS_MAX = 4,
   // examples/llm/qwen3.py:215-230) dequantizes to x's type and multiplies.
-  // Up to 64 rows of int4 u32x8 codes stream through MFMA with the codes
-  // kept factored per group (qskinny.hip); otherwise dequantize and
-  // multiply in one fused MFMA GEMM (qgemm.hip).
+  // Up to 64 rows of int4 (32 of int8) codes stream through MFMA with the
+  // codes kept factored per group (qskinny.hip); up to 128 rows dequantize
+  // in registers with K split over the waves of a workgroup (qmid.hip);
+  // otherwise dequantize and multiply in one fused MFMA GEMM (qgemm.hip).
   if (m > 4 && QSkinnyApplies(p)) return LaunchQSkinny(p, stream);
+  if (m > 4 && QMidApplies(p)) return LaunchQMid(p, stream);
   if (m > 4 && QGemmApplies(p)) return LaunchQGemm(p, stream);
   if (m <= 4) {
     const int cus = DeviceComputeUnits();

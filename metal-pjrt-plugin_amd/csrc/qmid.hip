@@ -1,0 +1,332 @@
+// Quantized matmul for a medium number of rows of x (33..128 as routed):
+// y[M, N] = x[M, K] W^T, W int8 (u8 affine or s8 symmetric) or int4 (u32x8
+// words), bf16 x / scale / offset, group size 64 — the short-prefill
+// shapes. The reference's linear() (examples/llm/qwen3.py:215-230)
+// dequantizes W to x's type for more than ROWS_MAX = 4 rows
+// (dequantize, qwen3.py:199-207) and multiplies; this kernel does the same
+// per weight, in registers, and never writes the dequantized weights.
+//
+// Design (MI355X-first). At these M the work sits near the ridge point:
+// for 128 x 12288 x 4096 int8 the 50 MB of codes take ~7 us at HBM speed
+// and the 12.9 GFLOP ~6 us on the matrix cores, and only 1.5 M outputs
+// exist, i.e. ~6000 per CU. So:
+//  - A workgroup owns NR = 16 NB weight rows and all M rows of x (a
+//    16 MB x NR output tile, 128 x 48 for that shape: 256 workgroups, one
+//    per CU), and its KW waves split K (each wave a contiguous run of
+//    groups). Every weight is loaded and dequantized exactly once, and
+//    each wave fetches a distinct slice of x, so no operand byte is
+//    fetched twice by a workgroup. The KW partial tiles are summed
+//    through LDS at the end.
+//  - v_mfma_f32_16x16x32_bf16, A = 16 rows of x, B = 16 weight rows. The
+//    K order inside a group is permuted identically for x and W (MFMA
+//    sums over K, so only the pairing matters): lane l takes codes
+//    16 (l / 16) .. + 15 of the group (one contiguous 16-byte or 8-byte
+//    load per weight row) and the matching 32 contiguous bytes of x; codes
+//    0..7 of the run feed the group's first MFMA, 8..15 its second.
+//  - Weights are dequantized in registers as bf16(q s + b) (one fma per
+//    weight, then one rounding to bf16; the reference's XLA program rounds
+//    q s and q s + b to bf16 separately, a difference far inside the
+//    matmul tolerance).
+//  - Loads go straight to registers, the next group in flight while one is
+//    computed (each load issued unconditionally; groups past the wave's
+//    run read zeros through out-of-range offsets), so the in-order memory
+//    counter waits only for the group being consumed.
+//  - Rows past M or N read zeros through buffer descriptors and are not
+//    stored.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "qk_device.h"
+#include "qk_internal.h"
+
+namespace qk {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+struct MdArgs {
+  const void* x;
+  const void* codes;
+  const void* scales;
+  const void* biases;
+  void* y;
+  int m, n, k;
+  int groups;  // k / 64
+  int has_bias;
+  int gpw;     // groups per wave
+};
+
+constexpr int kNonTemporal = 2;
+constexpr int kOut = 0x7FFF0000;  // an offset past every extent
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t Rsrc(const void* p,
+                                                       int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
+                                           bytes, 0x00020000);
+}
+
+// Eight codes -> bf16(q * s + b). int4: the 8 nibbles of a u32x8 word, code
+// j at bits 4 j; int8: 8 bytes (s8: signed).
+template <int PACK>
+__device__ __forceinline__ bf16x8 Dequant8(uint32_t w0, uint32_t w1, float s,
+                                           float b) {
+  bf16x8 r;
+  if constexpr (PACK == QK_PACK_U32X8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      r[j] = from_f32<bf16>(
+          fmaf(static_cast<float>((w0 >> (4 * j)) & 15u), s, b));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t w = j < 4 ? w0 : w1;
+      const uint32_t byte = (w >> (8 * (j & 3))) & 255u;
+      const float q = PACK == QK_PACK_S8_SYM
+                          ? static_cast<float>(static_cast<int8_t>(byte))
+                          : static_cast<float>(byte);
+      r[j] = from_f32<bf16>(fmaf(q, s, b));
+    }
+  }
+  return r;
+}
+
+template <int PACK, int MB, int NB, int KW>
+__global__ __launch_bounds__(KW * 64) void qmm_mid_kernel(MdArgs a) {
+  constexpr bool kInt4 = PACK == QK_PACK_U32X8;
+  constexpr int GB = kInt4 ? 32 : 64;  // code bytes per group per row
+  constexpr int NR = 16 * NB;          // weight rows per workgroup
+  constexpr int TM = 16 * MB, TS = NR + 1;
+  constexpr int kXSlot = TM * 128;     // one wave's x slice of one group
+  constexpr int kHalfWaves = (KW + 1) / 2;
+  constexpr int kPart = kHalfWaves * TM * TS * 4;
+  constexpr int kArr = KW * kXSlot > kPart ? KW * kXSlot : kPart;
+  // Ring slots 0 and 1 of every wave's x (separate arrays: the compiler's
+  // wait for an LDS DMA is per array, so reading slot 0 never waits for
+  // the DMA into slot 1); after the loop, the partial tiles.
+  __shared__ __attribute__((aligned(16))) unsigned char st0[kArr];
+  __shared__ __attribute__((aligned(16))) unsigned char st1[kArr];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q16 = lane >> 4, l16 = lane & 15;
+  const int n0 = blockIdx.x * NR;
+  const int G = a.groups;
+  const int row_bytes = kInt4 ? a.k / 2 : a.k;
+  const auto crs = Rsrc(a.codes, a.n * row_bytes);
+  const auto xrs = Rsrc(a.x, a.m * a.k * 2);
+  const auto srs = Rsrc(a.scales, a.n * G * 2);
+  const auto brs = Rsrc(a.biases, a.has_bias ? a.n * G * 2 : 0);
+
+  // Codes: lane l covers weight row 16 nb + l % 16, GB / 4 bytes at
+  // GB / 4 * (l / 16) of each group (16 codes).
+  int cvo[NB], svo[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int r = n0 + 16 * nb + l16;
+    cvo[nb] = r < a.n ? r * row_bytes + (GB / 4) * q16 : kOut;
+    svo[nb] = r < a.n ? r * G * 2 : kOut;
+  }
+  // x: a group's slice (TM rows x 128 bytes) goes into the wave's LDS slot
+  // with TM / 8 DMA instructions; instruction i, lane L: row 8 i + L / 8,
+  // its 16-byte chunk (L % 8) ^ (L / 8) into slot L % 8 of the row (the
+  // slot of chunk c of row r is c ^ (r & 7)). Consecutive lanes read
+  // consecutive bytes of one row; rows past M lie past the descriptor's
+  // extent and read zeros.
+  const int xvo = ((lane >> 3) * a.k + ((lane & 7) ^ (lane >> 3)) * 8) * 2;
+  unsigned char* const xs0 = st0 + wave * kXSlot;
+  unsigned char* const xs1 = st1 + wave * kXSlot;
+
+  struct Grp {
+    u32x2 c8[kInt4 ? NB : 1];   // int4: 16 codes in two words
+    u32x4 c16[kInt4 ? 1 : NB];  // int8: 16 bytes
+    uint32_t s[NB], b[NB];      // bf16 bits, zero-extended
+  };
+  const int g0 = wave * a.gpw;
+  // Group gi of the wave's run (past the run: zeros, no memory traffic).
+  auto load = [&](int gi, unsigned char* xdst, Grp& t) {
+    const int oob = gi < a.gpw ? 0 : kOut;
+    const int g = g0 + min(gi, a.gpw - 1);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      if constexpr (kInt4)
+        t.c8[nb] = __builtin_amdgcn_raw_buffer_load_b64(crs, cvo[nb] + oob,
+                                                        g * GB, kNonTemporal);
+      else
+        t.c16[nb] = __builtin_amdgcn_raw_buffer_load_b128(
+            crs, cvo[nb] + oob, g * GB, kNonTemporal);
+      t.s[nb] = __builtin_amdgcn_raw_buffer_load_b16(srs, svo[nb] + oob, g * 2, 0);
+      t.b[nb] = __builtin_amdgcn_raw_buffer_load_b16(brs, svo[nb] + oob, g * 2, 0);
+    }
+    using LdsPtr = __attribute__((address_space(3))) void*;
+#pragma unroll
+    for (int i = 0; i < TM / 8; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xrs, (LdsPtr)(xdst + i * 1024), 16,
+          xvo + i * 8 * a.k * 2 + oob, g * 128, 0, 0);
+  };
+
+  f32x4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // x fragment of row block mb, half h (K chunk 2 (l / 16) + h of the
+  // lane's row) from the wave's slot.
+  auto xfrag = [&](const unsigned char* xsl, int mb, int h) {
+    const int r = 16 * mb + l16;
+    const int c = 2 * q16 + h;
+    return *reinterpret_cast<const bf16x8*>(xsl + r * 128 +
+                                            ((c ^ (r & 7)) << 4));
+  };
+  auto process = [&](const unsigned char* xsl, const Grp& t) {
+    bf16x8 w[NB][2];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const float sc = __uint_as_float(t.s[nb] << 16);
+      const float bi = __uint_as_float(t.b[nb] << 16);
+      if constexpr (kInt4) {
+        w[nb][0] = Dequant8<PACK>(t.c8[nb][0], 0u, sc, bi);
+        w[nb][1] = Dequant8<PACK>(t.c8[nb][1], 0u, sc, bi);
+      } else {
+        w[nb][0] = Dequant8<PACK>(t.c16[nb][0], t.c16[nb][1], sc, bi);
+        w[nb][1] = Dequant8<PACK>(t.c16[nb][2], t.c16[nb][3], sc, bi);
+      }
+    }
+    // All first-half MFMAs, then all second-half ones: the two MFMAs
+    // into one accumulator are NB * MB instructions apart.
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const bf16x8 xv = xfrag(xsl, mb, h);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              xv, w[nb][h], acc[mb][nb], 0, 0, 0);
+      }
+  };
+
+  // Two groups in flight (slots 0 and 1 alternate). A group is TM / 8 + 3
+  // NB memory operations per lane and the memory counter tracks at most
+  // 63. The run is padded to an even length with groups past it, which
+  // read zeros (codes, x, scales and offsets) and so add nothing: the loop
+  // body has no branch (a conditional process makes the compiler's
+  // wait-count pass drain every load at the loop head). The scheduling
+  // barriers keep each group's loads ahead of the previous group's
+  // arithmetic. A wave's LDS slot is its own, so no workgroup barrier is
+  // needed: its reads of a slot are consumed by its MFMAs before it issues
+  // the next DMA into that slot.
+  static_assert(2 * (TM / 8 + 3 * NB) <= 63, "memory counter");
+  Grp A, B;
+  load(0, xs0, A);
+  for (int gi = 0; gi < a.gpw; gi += 2) {
+    load(gi + 1, xs1, B);
+    __builtin_amdgcn_sched_barrier(0);
+    process(xs0, A);
+    load(gi + 2, xs0, A);
+    __builtin_amdgcn_sched_barrier(0);
+    process(xs1, B);
+  }
+
+  // Sum the KW partial tiles (half of them in each array, after the last
+  // DMA, which writes zeros, has landed) and store rows < M, columns < N.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  float* const p0 = reinterpret_cast<float*>(st0);
+  float* const p1 = reinterpret_cast<float*>(st1);
+  float* const mine = (wave < kHalfWaves ? p0 : p1) +
+                      (wave % kHalfWaves) * TM * TS;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        mine[(16 * mb + 4 * q16 + r) * TS + 16 * nb + l16] = acc[mb][nb][r];
+  __syncthreads();
+  bf16* Y = static_cast<bf16*>(a.y);
+  for (int e = threadIdx.x; e < TM * NR; e += KW * 64) {
+    const int r = e / NR, c = e % NR;
+    if (r >= a.m || n0 + c >= a.n) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < KW; ++w)
+      v += (w < kHalfWaves ? p0 : p1)[((w % kHalfWaves) * TM + r) * TS + c];
+    Y[static_cast<long long>(r) * a.n + n0 + c] = from_f32<bf16>(v);
+  }
+}
+
+}  // namespace
+
+bool QMidApplies(const QuantProblem& p) {
+  const bool int4 = p.bits == 4 && p.packing == QK_PACK_U32X8;
+  const bool int8 = p.bits == 8 && (p.packing == QK_PACK_U8 ||
+                                    p.packing == QK_PACK_S8_SYM);
+  const int64_t row_bytes = int4 ? p.k / 2 : p.k;
+  return p.m >= 1 && p.m <= 128 && (int4 || int8) && p.group == 64 &&
+         p.x_dtype == QK_BF16 && p.scale_dtype == QK_BF16 &&
+         (!p.has_bias || p.bias_dtype == QK_BF16) && p.k % 256 == 0 &&
+         p.k > 0 && p.n > 0 && p.n * row_bytes < (int64_t{1} << 31) &&
+         p.m * p.k * 2 < (int64_t{1} << 31) &&
+         p.n * (p.k / 64) * 2 < (int64_t{1} << 31) &&
+         reinterpret_cast<uintptr_t>(p.x) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(p.codes) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(p.scales) % 2 == 0 &&
+         (!p.has_bias || reinterpret_cast<uintptr_t>(p.biases) % 2 == 0);
+}
+
+qk_status LaunchQMid(const QuantProblem& p, hipStream_t stream) {
+  MdArgs a;
+  a.x = p.x;
+  a.codes = p.codes;
+  a.scales = p.scales;
+  a.biases = p.has_bias ? p.biases : nullptr;
+  a.y = p.y;
+  a.m = static_cast<int>(p.m);
+  a.n = static_cast<int>(p.n);
+  a.k = static_cast<int>(p.k);
+  a.groups = a.k / 64;
+  a.has_bias = p.has_bias ? 1 : 0;
+  // Four K slices, one wave each (one per SIMD), one workgroup per CU.
+  constexpr int KW = 4;
+  a.gpw = a.groups / KW;  // k % 256 == 0
+  const int cus = DeviceComputeUnits();
+  // The widest tile (48, 32 or 16 weight rows) that still gives every CU
+  // a workgroup.
+  const int nb = (a.n + 47) / 48 >= cus ? 3 : (a.n + 31) / 32 >= cus ? 2 : 1;
+  const dim3 grid((a.n + 16 * nb - 1) / (16 * nb));
+  const int mb = (a.m + 15) / 16;
+#define QK_MID_NB(P, MB)                                                  \
+  do {                                                                    \
+    if (nb == 3)                                                          \
+      qmm_mid_kernel<P, MB, 3, KW><<<grid, KW * 64, 0, stream>>>(a);      \
+    else if (nb == 2)                                                     \
+      qmm_mid_kernel<P, MB, 2, KW><<<grid, KW * 64, 0, stream>>>(a);      \
+    else                                                                  \
+      qmm_mid_kernel<P, MB, 1, KW><<<grid, KW * 64, 0, stream>>>(a);      \
+  } while (0)
+#define QK_MID(P)                                                         \
+  do {                                                                    \
+    if (mb <= 4) QK_MID_NB(P, 4);                                         \
+    else if (mb <= 6) QK_MID_NB(P, 6);                                    \
+    else QK_MID_NB(P, 8);                                                 \
+  } while (0)
+  if (p.packing == QK_PACK_U32X8)
+    QK_MID(QK_PACK_U32X8);
+  else if (p.packing == QK_PACK_U8)
+    QK_MID(QK_PACK_U8);
+  else
+    QK_MID(QK_PACK_S8_SYM);
+#undef QK_MID
+#undef QK_MID_NB
+  return PostLaunch("qmm_mid");
+}
+
+}  // namespace qk

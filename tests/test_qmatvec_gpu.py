@@ -144,6 +144,34 @@ def test_qmatvec_few_rows(dev, mnk, packing):
         check_matvec(y.float().cpu().numpy().astype(np.float64), x, w)
 
 
+@pytest.mark.parametrize("mnk", [(65, 64, 256), (100, 1000, 1024),
+                                 (128, 3000, 4096), (128, 12288, 512),
+                                 (80, 8192, 768), (33, 4100, 2048)])
+@pytest.mark.parametrize("packing", [Packing.U32X8, Packing.U8,
+                                     Packing.S8_SYM])
+def test_qmatvec_mid_rows(dev, mnk, packing):
+    """33..128 rows (int8 beyond 32, int4 beyond 64): the kernel that
+    dequantizes in registers with K split over the waves of a workgroup —
+    16, 32 and 48 weight rows per workgroup (by N), 5..8 row blocks,
+    ragged M and N, one to sixteen groups per wave, with and without
+    offsets, elementwise against the float64 oracle (the weights rounded
+    to bf16 as the reference's dequantize does)."""
+    m, n, k = mnk
+    rng = np.random.default_rng(m * 13 + n + k)
+    for has_bias in (True, False):
+        dc, ds, db, w, *_ = make_weights(rng, n, k, packing, 64,
+                                         has_bias=has_bias)
+        x = O.round_to(rng.standard_normal((m, k)), "bfloat16").astype(
+            np.float32)
+        y = qkern.qmatvec(torch.from_numpy(x).to(torch.bfloat16).to(dev),
+                          dc.to(dev), ds.to(dev),
+                          None if db is None else db.to(dev),
+                          packing=packing)
+        torch.cuda.synchronize()
+        check_matvec(y.float().cpu().numpy().astype(np.float64), x,
+                     O.round_to(w, "bfloat16"))
+
+
 @pytest.mark.parametrize("case", [
     (256, 384, 1024, Packing.U32X8, "bfloat16"),
     (512, 1024, 2048, Packing.U8, "bfloat16"),
