@@ -71,6 +71,27 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t Rsrc(const void* p,
                                            bytes, 0x00020000);
 }
 
+// LDS DMA of 16 or 4 bytes per lane into lds + lane * size, as device-only
+// helpers (the address-space cast of the LDS pointer is not valid host
+// code). Dma16Nt reads nontemporally (streamed once).
+using LdsPtr = __attribute__((address_space(3))) void*;
+__device__ __forceinline__ void Dma16(__amdgpu_buffer_rsrc_t r,
+                                      unsigned char* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)lds, 16, voff, soff, 0,
+                                           0);
+}
+__device__ __forceinline__ void Dma16Nt(__amdgpu_buffer_rsrc_t r,
+                                        unsigned char* lds, int voff,
+                                        int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)lds, 16, voff, soff, 0,
+                                           kNonTemporal);
+}
+__device__ __forceinline__ void Dma4(__amdgpu_buffer_rsrc_t r,
+                                     unsigned char* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)lds, 4, voff, soff, 0,
+                                           0);
+}
+
 // Eight codes -> bf16(q * s + b). int4: the 8 nibbles of a u32x8 word, code
 // j at bits 4 j; int8: 8 bytes (s8: signed).
 template <int PACK>
@@ -102,13 +123,21 @@ __global__ __launch_bounds__(KW * 64) void qmm_mid_kernel(MdArgs a) {
   constexpr int GB = kInt4 ? 32 : 64;  // code bytes per group per row
   constexpr int NR = 16 * NB;          // weight rows per workgroup
   constexpr int TM = 16 * MB, TS = NR + 1;
-  constexpr int kXSlot = TM * 128;     // one wave's x slice of one group
+  static_assert(NR <= 64, "one scale DMA per group");
+  // A wave's slot for one group: x (TM rows x 128 bytes), codes (NR rows x
+  // GB bytes, whole 1 KB DMA instructions), scales and offsets (one dword
+  // per row: the group and its neighbour).
+  constexpr int kCRows = 1024 / GB;  // code rows per DMA instruction
+  constexpr int kCDma = (NR + kCRows - 1) / kCRows;
+  constexpr int kXOff = 0, kCOff = TM * 128, kSOff = kCOff + kCDma * 1024,
+                kBOff = kSOff + 256, kSlot = kBOff + 256;
+  constexpr int kDma = TM / 8 + kCDma + 2;  // DMA instructions per group
   constexpr int kHalfWaves = (KW + 1) / 2;
   constexpr int kPart = kHalfWaves * TM * TS * 4;
-  constexpr int kArr = KW * kXSlot > kPart ? KW * kXSlot : kPart;
-  // Ring slots 0 and 1 of every wave's x (separate arrays: the compiler's
-  // wait for an LDS DMA is per array, so reading slot 0 never waits for
-  // the DMA into slot 1); after the loop, the partial tiles.
+  constexpr int kArr = KW * kSlot > kPart ? KW * kSlot : kPart;
+  // Ring slots 0 and 1 of every wave (separate arrays: the compiler's wait
+  // for an LDS DMA is per array, so reading slot 0 never waits for the DMA
+  // into slot 1); after the loop, the partial tiles.
   __shared__ __attribute__((aligned(16))) unsigned char st0[kArr];
   __shared__ __attribute__((aligned(16))) unsigned char st1[kArr];
 
@@ -123,52 +152,45 @@ __global__ __launch_bounds__(KW * 64) void qmm_mid_kernel(MdArgs a) {
   const auto srs = Rsrc(a.scales, a.n * G * 2);
   const auto brs = Rsrc(a.biases, a.has_bias ? a.n * G * 2 : 0);
 
-  // Codes: lane l covers weight row 16 nb + l % 16, GB / 4 bytes at
-  // GB / 4 * (l / 16) of each group (16 codes).
-  int cvo[NB], svo[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int r = n0 + 16 * nb + l16;
-    cvo[nb] = r < a.n ? r * row_bytes + (GB / 4) * q16 : kOut;
-    svo[nb] = r < a.n ? r * G * 2 : kOut;
-  }
-  // x: a group's slice (TM rows x 128 bytes) goes into the wave's LDS slot
-  // with TM / 8 DMA instructions; instruction i, lane L: row 8 i + L / 8,
-  // its 16-byte chunk (L % 8) ^ (L / 8) into slot L % 8 of the row (the
-  // slot of chunk c of row r is c ^ (r & 7)). Consecutive lanes read
-  // consecutive bytes of one row; rows past M lie past the descriptor's
-  // extent and read zeros.
+  // Every DMA instruction writes 16 (4) bytes per lane at lane * 16 (4) of
+  // its destination; the lanes are mapped so that consecutive lanes read
+  // consecutive bytes of one row, and rows past M / N read zeros.
+  //  x, instruction i: row 8 i + L / 8, 16-byte chunk (L % 8) ^ (L / 8)
+  //    into slot L % 8 (the slot of chunk c of row r is c ^ (r & 7)).
   const int xvo = ((lane >> 3) * a.k + ((lane & 7) ^ (lane >> 3)) * 8) * 2;
-  unsigned char* const xs0 = st0 + wave * kXSlot;
-  unsigned char* const xs1 = st1 + wave * kXSlot;
+  //  codes, instruction i: row kCRows i + L / (GB / 16), 16-byte chunk
+  //    p ^ sw(row) into slot p = L % (GB / 16), with sw(r) = (r / 2) & 3
+  //    for int8 (64-byte rows) and (r / 4) & 1 for int4 (32-byte rows).
+  int cvo[kCDma];
+#pragma unroll
+  for (int i = 0; i < kCDma; ++i) {
+    constexpr int LPR = GB / 16;
+    const int rr = kCRows * i + lane / LPR;
+    const int sw = kInt4 ? ((rr >> 2) & 1) : ((rr >> 1) & 3);
+    const int r = n0 + rr;
+    cvo[i] = (rr < NR && r < a.n)
+                 ? r * row_bytes + (((lane % LPR) ^ sw) << 4)
+                 : kOut;
+  }
+  //  scales / offsets: lane L < NR, row n0 + L, the dword holding groups
+  //    g & ~1 and (g & ~1) + 1.
+  const int svo = (lane < NR && n0 + lane < a.n) ? (n0 + lane) * G * 2 : kOut;
 
-  struct Grp {
-    u32x2 c8[kInt4 ? NB : 1];   // int4: 16 codes in two words
-    u32x4 c16[kInt4 ? 1 : NB];  // int8: 16 bytes
-    uint32_t s[NB], b[NB];      // bf16 bits, zero-extended
-  };
   const int g0 = wave * a.gpw;
-  // Group gi of the wave's run (past the run: zeros, no memory traffic).
-  auto load = [&](int gi, unsigned char* xdst, Grp& t) {
+  // DMA group gi of the wave's run into slot (past the run: zeros).
+  auto load = [&](int gi, unsigned char* slot) {
     const int oob = gi < a.gpw ? 0 : kOut;
     const int g = g0 + min(gi, a.gpw - 1);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      if constexpr (kInt4)
-        t.c8[nb] = __builtin_amdgcn_raw_buffer_load_b64(crs, cvo[nb] + oob,
-                                                        g * GB, kNonTemporal);
-      else
-        t.c16[nb] = __builtin_amdgcn_raw_buffer_load_b128(
-            crs, cvo[nb] + oob, g * GB, kNonTemporal);
-      t.s[nb] = __builtin_amdgcn_raw_buffer_load_b16(srs, svo[nb] + oob, g * 2, 0);
-      t.b[nb] = __builtin_amdgcn_raw_buffer_load_b16(brs, svo[nb] + oob, g * 2, 0);
-    }
-    using LdsPtr = __attribute__((address_space(3))) void*;
+    for (int i = 0; i < kCDma; ++i)
+      Dma16Nt(crs, slot + kCOff + i * 1024, cvo[i] + oob,
+                            g * GB);
+    Dma4(srs, slot + kSOff, svo + oob, (g & ~1) * 2);
+    Dma4(brs, slot + kBOff, svo + oob, (g & ~1) * 2);
 #pragma unroll
     for (int i = 0; i < TM / 8; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          xrs, (LdsPtr)(xdst + i * 1024), 16,
-          xvo + i * 8 * a.k * 2 + oob, g * 128, 0, 0);
+      Dma16(xrs, slot + kXOff + i * 1024, xvo + i * 8 * a.k * 2 + oob,
+                 g * 128);
   };
 
   f32x4 acc[MB][NB];
@@ -177,35 +199,45 @@ __global__ __launch_bounds__(KW * 64) void qmm_mid_kernel(MdArgs a) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // x fragment of row block mb, half h (K chunk 2 (l / 16) + h of the
-  // lane's row) from the wave's slot.
-  auto xfrag = [&](const unsigned char* xsl, int mb, int h) {
-    const int r = 16 * mb + l16;
-    const int c = 2 * q16 + h;
-    return *reinterpret_cast<const bf16x8*>(xsl + r * 128 +
-                                            ((c ^ (r & 7)) << 4));
-  };
-  auto process = [&](const unsigned char* xsl, const Grp& t) {
+  auto process = [&](const unsigned char* slot, int gi) {
+    const int odd = (g0 + min(gi, a.gpw - 1)) & 1;
     bf16x8 w[NB][2];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      const float sc = __uint_as_float(t.s[nb] << 16);
-      const float bi = __uint_as_float(t.b[nb] << 16);
+      const int r = 16 * nb + l16;
+      const float sc = __uint_as_float(static_cast<uint32_t>(
+          *reinterpret_cast<const uint16_t*>(slot + kSOff + r * 4 + odd * 2))
+          << 16);
+      const float bi = __uint_as_float(static_cast<uint32_t>(
+          *reinterpret_cast<const uint16_t*>(slot + kBOff + r * 4 + odd * 2))
+          << 16);
       if constexpr (kInt4) {
-        w[nb][0] = Dequant8<PACK>(t.c8[nb][0], 0u, sc, bi);
-        w[nb][1] = Dequant8<PACK>(t.c8[nb][1], 0u, sc, bi);
+        // the lane's 16 codes: bytes 8 (l / 16) .. + 7 of the row
+        const int slt = (q16 >> 1) ^ ((r >> 2) & 1);
+        const u32x2 c = *reinterpret_cast<const u32x2*>(
+            slot + kCOff + r * GB + (slt << 4) + ((q16 & 1) << 3));
+        w[nb][0] = Dequant8<PACK>(c[0], 0u, sc, bi);
+        w[nb][1] = Dequant8<PACK>(c[1], 0u, sc, bi);
       } else {
-        w[nb][0] = Dequant8<PACK>(t.c16[nb][0], t.c16[nb][1], sc, bi);
-        w[nb][1] = Dequant8<PACK>(t.c16[nb][2], t.c16[nb][3], sc, bi);
+        // the lane's 16 codes: chunk l / 16 of the row
+        const int slt = q16 ^ ((r >> 1) & 3);
+        const u32x4 c = *reinterpret_cast<const u32x4*>(
+            slot + kCOff + r * GB + (slt << 4));
+        w[nb][0] = Dequant8<PACK>(c[0], c[1], sc, bi);
+        w[nb][1] = Dequant8<PACK>(c[2], c[3], sc, bi);
       }
     }
     // All first-half MFMAs, then all second-half ones: the two MFMAs
-    // into one accumulator are NB * MB instructions apart.
+    // into one accumulator are NB * MB instructions apart. x fragment of
+    // row block mb, half h: K chunk 2 (l / 16) + h of the lane's row.
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const bf16x8 xv = xfrag(xsl, mb, h);
+        const int r = 16 * mb + l16;
+        const int c = 2 * q16 + h;
+        const bf16x8 xv = *reinterpret_cast<const bf16x8*>(
+            slot + kXOff + r * 128 + ((c ^ (r & 7)) << 4));
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
           acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -213,26 +245,36 @@ __global__ __launch_bounds__(KW * 64) void qmm_mid_kernel(MdArgs a) {
       }
   };
 
-  // Two groups in flight (slots 0 and 1 alternate). A group is TM / 8 + 3
-  // NB memory operations per lane and the memory counter tracks at most
-  // 63. The run is padded to an even length with groups past it, which
-  // read zeros (codes, x, scales and offsets) and so add nothing: the loop
-  // body has no branch (a conditional process makes the compiler's
-  // wait-count pass drain every load at the loop head). The scheduling
-  // barriers keep each group's loads ahead of the previous group's
-  // arithmetic. A wave's LDS slot is its own, so no workgroup barrier is
-  // needed: its reads of a slot are consumed by its MFMAs before it issues
-  // the next DMA into that slot.
-  static_assert(2 * (TM / 8 + 3 * NB) <= 63, "memory counter");
-  Grp A, B;
-  load(0, xs0, A);
+  // Two groups in flight (slots 0 and 1 alternate); the memory counter
+  // tracks at most 63 operations. The run is padded to an even length with
+  // groups past it, which read zeros (codes, x, scales and offsets) and so
+  // add nothing: the loop body has no branch (a conditional process makes
+  // the compiler's wait-count pass drain every load at the loop head). The
+  // scheduling barriers keep each group's DMA ahead of the previous
+  // group's arithmetic. A wave's slots are its own, so no workgroup
+  // barrier is needed: its LDS reads of a slot are consumed by its MFMAs
+  // before it issues the next DMA into that slot.
+  //
+  // The wait for a slot's DMA is explicit: vmcnt(kDma) after the next
+  // group's DMA has been issued means every DMA into the slot about to be
+  // read has landed. It is written as asm with a memory clobber (no LDS
+  // read moves above it): the compiler's own tracking of LDS DMA cannot be
+  // relied on here (its memory operand describes 16 bytes at the wave's
+  // base address, not the 1 KB the instruction writes, so reads of other
+  // rows of the slot were found to get no wait).
+  static_assert(2 * kDma <= 63, "memory counter");
+  unsigned char* const sl0 = st0 + wave * kSlot;
+  unsigned char* const sl1 = st1 + wave * kSlot;
+  load(0, sl0);
   for (int gi = 0; gi < a.gpw; gi += 2) {
-    load(gi + 1, xs1, B);
+    load(gi + 1, sl1);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDma) : "memory");
     __builtin_amdgcn_sched_barrier(0);
-    process(xs0, A);
-    load(gi + 2, xs0, A);
+    process(sl0, gi);
+    load(gi + 2, sl0);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDma) : "memory");
     __builtin_amdgcn_sched_barrier(0);
-    process(xs1, B);
+    process(sl1, gi + 1);
   }
 
   // Sum the KW partial tiles (half of them in each array, after the last
@@ -278,8 +320,8 @@ bool QMidApplies(const QuantProblem& p) {
          p.n * (p.k / 64) * 2 < (int64_t{1} << 31) &&
          reinterpret_cast<uintptr_t>(p.x) % 16 == 0 &&
          reinterpret_cast<uintptr_t>(p.codes) % 16 == 0 &&
-         reinterpret_cast<uintptr_t>(p.scales) % 2 == 0 &&
-         (!p.has_bias || reinterpret_cast<uintptr_t>(p.biases) % 2 == 0);
+         reinterpret_cast<uintptr_t>(p.scales) % 4 == 0 &&
+         (!p.has_bias || reinterpret_cast<uintptr_t>(p.biases) % 4 == 0);
 }
 
 qk_status LaunchQMid(const QuantProblem& p, hipStream_t stream) {
