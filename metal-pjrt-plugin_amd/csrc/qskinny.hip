@@ -14,7 +14,10 @@
 //    (reduced through LDS at the end). Each wave walks its K slice in
 //    sub-chunks of CG groups: the sub-chunk's codes are read as contiguous
 //    row segments (32 CG bytes per row, 16 bytes per lane) and reach the
-//    MFMA layout through a wave-private LDS buffer (a wave's LDS
+//    MFMA layout through a wave-private LDS buffer, and so does the
+//    sub-chunk's x (16 bytes per lane along a row: with one row per lane,
+//    as the MFMA layout has it, every four lanes would touch four rows,
+//    which measured ~4x slower to issue) (a wave's LDS
 //    operations run in order, so each sub-chunk is written over the last
 //    after its final read). Scales, offsets and the sub-chunk's x travel
 //    with the codes: the next sub-chunk is requested as a whole while the
@@ -110,6 +113,19 @@ __device__ __forceinline__ bf16x8 CodeBytes(uint32_t w0, uint32_t w1) {
   return r;
 }
 
+// LDS bytes of qmm_skinny_kernel (per wave: codes, scales/offsets and x
+// buffers; after the loop, the KW partial tiles).
+template <int PACK, int MB, int NB, int KW, int CG>
+constexpr int SkinnyLdsBytes() {
+  constexpr int GB = PACK == QK_PACK_U32X8 ? 32 : 64;
+  constexpr int NR = 16 * NB;
+  constexpr int wave = NR * (GB * CG + 16) + 2 * NR * CG * 2 +
+                       16 * MB * (CG * 128 + 16);
+  constexpr int part = KW * (16 * MB) * (NR + 1) * 4;
+  return KW * wave > part ? KW * wave : part;
+}
+constexpr int kMaxLds = 160 * 1024;
+
 template <int PACK, int MB, int NB, int KW, int CG>
 __global__ __launch_bounds__(KW * 64) void qmm_skinny_kernel(SkArgs a) {
   constexpr bool kInt4 = PACK == QK_PACK_U32X8;
@@ -121,7 +137,20 @@ __global__ __launch_bounds__(KW * 64) void qmm_skinny_kernel(SkArgs a) {
   constexpr int CL = NR / RPL;          // code loads per sub-chunk
   constexpr int kRow = SEG + 16;        // LDS row stride (padded)
   constexpr int kBuf = NR * kRow;
-  constexpr int kWaveBytes = kBuf + 2 * NR * CG * 2;
+  // x of one sub-chunk (16 MB rows x CG groups of 128 bytes) is loaded
+  // row-contiguously (consecutive lanes, consecutive 16 bytes of one row)
+  // and reaches the MFMA layout through the wave's LDS buffer, rows padded
+  // by 16 bytes (the 16 rows a fragment read touches fall in distinct
+  // banks).
+  constexpr int XB = CG * 128;          // x bytes per row per sub-chunk
+  constexpr int XLPR = XB / 16;         // lanes per row in an x load
+  constexpr int XRPL = 64 / XLPR;       // rows per x load
+  constexpr int XL = 16 * MB / XRPL;    // x loads per sub-chunk
+  constexpr int kXRow = XB + 16;
+  constexpr int kXBuf = 16 * MB * kXRow;
+  constexpr int kWaveBytes = kBuf + 2 * NR * CG * 2 + kXBuf;
+  static_assert(XL >= 1 && 64 % XLPR == 0, "x tile");
+  static_assert(SkinnyLdsBytes<PACK, MB, NB, KW, CG>() <= kMaxLds, "LDS");
   constexpr int kPartBytes = KW * (16 * MB) * (NR + 1) * 4;
   static_assert(CL >= 1 && NR % RPL == 0, "tile");
   __shared__ __attribute__((aligned(16)))
@@ -135,6 +164,7 @@ __global__ __launch_bounds__(KW * 64) void qmm_skinny_kernel(SkArgs a) {
   const int G = a.groups;
   unsigned char* const code_buf = lds + wave * kWaveBytes;
   uint16_t* const sb_buf = reinterpret_cast<uint16_t*>(code_buf + kBuf);
+  unsigned char* const x_buf = code_buf + kBuf + 2 * NR * CG * 2;
 
   const int row_bytes = kInt4 ? a.k / 2 : a.k;
   const auto crs = Rsrc(a.codes, a.n * row_bytes);
@@ -155,19 +185,19 @@ __global__ __launch_bounds__(KW * 64) void qmm_skinny_kernel(SkArgs a) {
   const bool sb_lane = lane < NR;
   const int sb_row = n0 + lane;
   const int svo = (sb_lane && sb_row < a.n) ? sb_row * G * 2 : kOut;
-  // x loads: lane l -> row 16 mb + l % 16, 32 bytes at K offset 16 (l / 16)
-  // of each group.
-  int xvo[MB];
+  // x loads: load i, lane l -> row XRPL i + l / XLPR, 16 bytes at
+  // 16 (l % XLPR) of the row's sub-chunk segment.
+  int xvo[XL];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int r = 16 * mb + l16;
-    xvo[mb] = r < a.m ? r * a.k * 2 + 32 * q16 : kOut;
+  for (int i = 0; i < XL; ++i) {
+    const int r = XRPL * i + lane / XLPR;
+    xvo[i] = r < a.m ? r * a.k * 2 + 16 * (lane % XLPR) : kOut;
   }
 
   struct Chunk {
     u32x4 c[CL];
     uint32_t s[CG / 2], b[CG / 2];
-    u32x4 x[CG][MB][2];
+    u32x4 x[XL];
   };
   // `skip`: sub-chunks past the slice read zeros (offsets past the extents).
   auto load = [&](int ch, bool skip, Chunk& t) {
@@ -187,13 +217,9 @@ __global__ __launch_bounds__(KW * 64) void qmm_skinny_kernel(SkArgs a) {
       t.b[0] = __builtin_amdgcn_raw_buffer_load_b32(brs, svo + oob, ch * 4, 0);
     }
 #pragma unroll
-    for (int gg = 0; gg < CG; ++gg)
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2)
-          t.x[gg][mb][t2] = __builtin_amdgcn_raw_buffer_load_b128(
-              xrs, xvo[mb] + oob + 16 * t2, (ch * CG + gg) * 128, 0);
+    for (int i = 0; i < XL; ++i)
+      t.x[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xvo[i] + oob,
+                                                     ch * XB, 0);
   };
 
   f32x4 acc[MB][NB];
@@ -219,6 +245,12 @@ __global__ __launch_bounds__(KW * 64) void qmm_skinny_kernel(SkArgs a) {
 #pragma unroll
       for (int h = 0; h < CG / 2; ++h) ds[h] = t.s[h], db[h] = t.b[h];
     }
+    // x rows into the wave's x buffer (after this wave's reads of the
+    // previous sub-chunk: a wave's LDS operations run in order)
+#pragma unroll
+    for (int i = 0; i < XL; ++i)
+      *reinterpret_cast<u32x4*>(x_buf + (XRPL * i + lane / XLPR) * kXRow +
+                                16 * (lane % XLPR)) = t.x[i];
 #pragma unroll
     for (int gg = 0; gg < CG; ++gg) {
       bf16x8 xa[MB][2];
@@ -229,8 +261,10 @@ __global__ __launch_bounds__(KW * 64) void qmm_skinny_kernel(SkArgs a) {
 #pragma unroll
         for (int t2 = 0; t2 < 2; ++t2) {
           // int4: x in the pair order of the code words; int8: as loaded
-          xa[mb][t2] = kInt4 ? XPairs(t.x[gg][mb][t2])
-                             : __builtin_bit_cast(bf16x8, t.x[gg][mb][t2]);
+          const u32x4 xv = *reinterpret_cast<const u32x4*>(
+              x_buf + (16 * mb + l16) * kXRow + gg * 128 + 32 * q16 +
+              16 * t2);
+          xa[mb][t2] = kInt4 ? XPairs(xv) : __builtin_bit_cast(bf16x8, xv);
           xs[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[mb][t2], ones,
                                                            xs[mb], 0, 0, 0);
         }
@@ -307,6 +341,16 @@ __global__ __launch_bounds__(KW * 64) void qmm_skinny_kernel(SkArgs a) {
   }
 }
 
+// The eight-wave kernel, or null when its LDS would exceed the limit.
+template <int PACK, int MB, int NB, int CG>
+auto Skinny8() {
+  using K = decltype(&qmm_skinny_kernel<PACK, MB, NB, 4, CG>);
+  if constexpr (SkinnyLdsBytes<PACK, MB, NB, 8, CG>() <= kMaxLds)
+    return static_cast<K>(&qmm_skinny_kernel<PACK, MB, NB, 8, CG>);
+  else
+    return static_cast<K>(nullptr);
+}
+
 }  // namespace
 
 bool QSkinnyApplies(const QuantProblem& p) {
@@ -359,9 +403,10 @@ qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream) {
   const dim3 grid((a.n + nr - 1) / nr);
   // The most waves per workgroup (8, 4 or 2) for which every workgroup is
   // resident at once (no second, partly empty round) and k splits evenly.
+  // k8 is null when eight waves would exceed the LDS (not instantiated).
   auto go = [&](auto k8, auto k4, auto k2) {
     auto fits = [&](const void* f, int waves) {
-      return a.k % (waves * 64 * cg) == 0 &&
+      return f != nullptr && a.k % (waves * 64 * cg) == 0 &&
              static_cast<int64_t>(ResidentBlocks(f, waves * 64, 0)) * cus >=
                  grid.x;
     };
@@ -379,8 +424,8 @@ qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream) {
       k2<<<grid, 2 * 64, 0, stream>>>(a);
   };
 #define QK_SKINNY(P, MB, NB, CG)                                         \
-  go(qmm_skinny_kernel<P, MB, NB, 8, CG>,                                \
-     qmm_skinny_kernel<P, MB, NB, 4, CG>, qmm_skinny_kernel<P, MB, NB, 2, CG>)
+  go(Skinny8<P, MB, NB, CG>(), qmm_skinny_kernel<P, MB, NB, 4, CG>,     \
+     qmm_skinny_kernel<P, MB, NB, 2, CG>)
   if (p.packing == QK_PACK_U32X8) {
     switch (mb) {
       case 1:
