@@ -350,9 +350,14 @@ constexpr HalfTile kHalfTiles[] = {
     {256, 128, 2, 2},  // 7: interior-tile LDS-DMA kernel, 128 x 64 per wave
     {64, 64, 2, 2},    // 8: split-K, four waves each a quarter of K
     {32, 32, 2, 4},    // 9: split-K for up to 32 rows, eight waves
+    {256, 192, 2, 2},  // 10: interior-tile LDS-DMA kernel, 128 x 96 per wave
 };
-constexpr int kFastTile256 = 6, kFastTile128 = 7, kSplitK = 8, kSplitK32 = 9;
+constexpr int kFastTile256 = 6, kFastTile128 = 7, kSplitK = 8, kSplitK32 = 9,
+              kFastTile192 = 10;
 constexpr int kNumHalfTiles = sizeof(kHalfTiles) / sizeof(kHalfTiles[0]);
+
+// Cost of a round of 256x192 interior tiles relative to 256x256.
+constexpr double kCost192 = 0.95;
 
 // QK_GEMM_TILE=<index into kHalfTiles> forces a configuration (tuning).
 int ForcedHalfTile() {
@@ -394,16 +399,26 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
   if (half) {
     int t = ForcedHalfTile();
     if ((t == kFastTile256 && !FastApplies(p, 256)) ||
+        (t == kFastTile192 && !FastApplies(p, 192)) ||
         (t == kFastTile128 && !FastApplies(p, 128)))
       t = -1;
     const int cus = DeviceComputeUnits();
-    if (t < 0 && FastApplies(p, 128) && tiles(256, 128) >= cus / 2) {
-      // One 256-row tile per CU. Measured on MI355X, a round of 256x128
-      // tiles costs ~0.67 of a round of 256x256 tiles.
-      const double r256 = static_cast<double>(CeilDiv(tiles(256, 256), cus));
-      const double r128 =
-          0.67 * static_cast<double>(CeilDiv(tiles(256, 128), cus));
-      t = FastApplies(p, 256) && r256 <= r128 ? kFastTile256 : kFastTile128;
+    if (t < 0) {
+      // One 256-row tile per CU: the fewest rounds of resident tiles,
+      // weighted by the cost of a round measured on MI355X relative to a
+      // round of 256x256 tiles (256x192 ~0.95, 256x128 ~0.67); a width
+      // qualifies when it gives at least half the CUs a tile.
+      double best = 1e30;
+      const struct { int bn, tile; double cost; } cand[] = {
+          {256, kFastTile256, 1.0},
+          {192, kFastTile192, kCost192},
+          {128, kFastTile128, 0.67}};
+      for (const auto& c : cand) {
+        if (!FastApplies(p, c.bn) || tiles(256, c.bn) < cus / 2) continue;
+        const double r =
+            c.cost * static_cast<double>(CeilDiv(tiles(256, c.bn), cus));
+        if (r < best) best = r, t = c.tile;
+      }
     }
     // Few 64x64 tiles and a long K: split K over the waves of each tile
     // (32x32 tiles and eight waves for at most 32 rows or columns).
@@ -431,7 +446,8 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
       c.bm = 64, c.bn = 64, c.bk = 32;
     }
   }
-  const bool fast = half && (c.tile == kFastTile256 || c.tile == kFastTile128);
+  const bool fast = half && (c.tile == kFastTile256 || c.tile == kFastTile192 ||
+                             c.tile == kFastTile128);
   const bool splitk = c.tile == kSplitK || c.tile == kSplitK32;
   c.name = std::string(splitk     ? (c.tile == kSplitK ? "gemm_splitk4_"
                                                        : "gemm_splitk8_")
@@ -465,6 +481,8 @@ qk_status DispatchHalf(int tile, const GemmArgs& g, int batch, bool ta,
       return DispatchFast<T, 256>(g, batch, ta, tb, st, name);
     case kFastTile128:
       return DispatchFast<T, 128>(g, batch, ta, tb, st, name);
+    case kFastTile192:
+      return DispatchFast<T, 192>(g, batch, ta, tb, st, name);
     case kSplitK:
       return DispatchSplitK<T, 64, 4>(g, batch, ta, tb, st, name);
     case kSplitK32:

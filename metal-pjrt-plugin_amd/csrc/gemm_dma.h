@@ -1,7 +1,7 @@
 // Interior-tile f16/bf16 GEMM whose operand tiles travel from global memory
 // straight into LDS (gfx950 `buffer_load_dwordx4 ... lds`), used by the
 // dense GEMM for problems whose M, N and K are multiples of 256 x BN x 64
-// (BN = 256 or 128) with 16-byte aligned operands. Replaces the tiled loop
+// (BN = 256, 192 or 128) with 16-byte aligned operands. Replaces the tiled loop
 // of the reference's steel GEMM (metal_pjrt/kernels/steel_gemm.metal:
 // 180-213) for those shapes; the store applies the same epilogue.
 //
@@ -145,6 +145,47 @@ struct DmaMN {
   }
 };
 
+// A 192-column M/N-contiguous tile as two DmaMN regions, columns 0..127
+// (256-byte K rows) and 128..191 (128-byte K rows): 4 + 2 DMA instructions
+// per wave. Every 32-column fragment lies in one region.
+template <typename T>
+struct DmaMN192 {
+  using Lo = DmaMN<T, 128>;
+  using Hi = DmaMN<T, 64>;
+  static constexpr int NI = Lo::NI + Hi::NI;
+  static constexpr int kBytes = Lo::kBytes + Hi::kBytes;
+  Lo lo;
+  Hi hi;
+  __device__ __forceinline__ void init(const T* src, long long bytes, int ld_,
+                                       int w, int lane) {
+    lo.init(src, bytes, ld_, w, lane);
+    hi.init(src, bytes, ld_, w, lane);
+  }
+  __device__ __forceinline__ void issue(unsigned char* lds, int r0, int k0,
+                                        int w, int i) const {
+    if (i < Lo::NI)
+      lo.issue(lds, r0, k0, w, i);
+    else
+      hi.issue(lds + Lo::kBytes, r0 + 128, k0, w, i - Lo::NI);
+  }
+  __device__ __forceinline__ static typename Frag<T>::type frag(
+      const unsigned char* lds, int rb, int kb, int lane) {
+    // rb is wave-uniform: pick the region without a branch
+    const bool h = rb >= 128;
+    const int RB = h ? Hi::RB : Lo::RB;
+    const unsigned char* base = h ? lds + Lo::kBytes : lds;
+    const int g = lane >> 4, s = lane & 15;
+    const int k = kb + 8 * (g >> 1) + (s >> 2);
+    const int n = (h ? rb - 128 : rb) + 16 * (g & 1) + 4 * (s & 3);
+    const unsigned char* p =
+        base + k * RB + (((n >> 3) ^ ((k & 3) << 1)) << 4) + (n & 7) * 2;
+    const u32x2 lo2 = lds_read_tr(reinterpret_cast<const T*>(p));
+    const u32x2 hi2 = lds_read_tr(reinterpret_cast<const T*>(p + 4 * RB));
+    const u32x4 q = {lo2[0], lo2[1], hi2[0], hi2[1]};
+    return __builtin_bit_cast(typename Frag<T>::type, q);
+  }
+};
+
 // s_waitcnt immediate for vmcnt(n) (expcnt, lgkmcnt not waited).
 constexpr int VmcntImm(int n) {
   return (n & 0xF) | (((n >> 4) & 3) << 14) | (7 << 4) | (0xF << 8);
@@ -155,7 +196,9 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs g) {
   constexpr int BM = 256, BK = 64, WM = 2, WN = 2;
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
   using LA = std::conditional_t<TA, DmaMN<T, BM>, DmaK<T, BM>>;
-  using LB = std::conditional_t<TB, DmaK<T, BN>, DmaMN<T, BN>>;
+  using LB = std::conditional_t<
+      TB, DmaK<T, BN>,
+      std::conditional_t<BN == 192, DmaMN192<T>, DmaMN<T, BN>>>;
   constexpr int kBOff = LA::kBytes;
   constexpr int kStage = LA::kBytes + LB::kBytes;
   constexpr int kDma = LA::NI + LB::NI;  // DMA instructions per wave per tile

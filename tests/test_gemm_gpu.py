@@ -189,6 +189,10 @@ def test_interior_tile_kernel(dev, ta, tb):
     # an odd number (5) of K tiles: the loop's unpaired last tile
     plan = run_case(dev, 4096, 2048, 320, ta=ta, tb=tb)
     assert "gemm_fast_bf16" in plan.describe()
+    # 256x192 tiles (384 tiles of 256x256 would be 1.5 rounds; 512 of
+    # 256x192 are 2): the two-region N-contiguous B tile in NN and TN
+    plan = run_case(dev, 2048, 12288, 192, ta=ta, tb=tb)
+    assert "gemm_fast_bf16_256x192" in plan.describe()
 
 
 def test_interior_tile_kernel_epilogues(dev):
@@ -202,6 +206,10 @@ def test_interior_tile_kernel_epilogues(dev):
     # batched with 8-element row padding (still 16-byte aligned rows)
     plan = run_case(dev, 1024, 2048, 128, batch=4, pad=8, beta=1.0)
     assert "gemm_fast" in plan.describe()
+    plan = run_case(dev, 2048, 12288, 64, tin="float16",
+                    epilogue=Epilogue.kBiasThenGELUWithAux, separate_c=True,
+                    beta=0.25)
+    assert "256x192" in plan.describe()
 
 
 def test_interior_tile_kernel_not_taken(dev):
