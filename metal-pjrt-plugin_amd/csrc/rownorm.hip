@@ -255,13 +255,41 @@ __global__ __launch_bounds__(kThreads) void rownorm_kernel(RnArgs a) {
 // per-row buffer descriptor whose extent is 0 for rows past the end
 // (loads read zeros, stores are dropped), so the loop has no branches
 // and the compiler's wait counts follow the two buffers exactly.
-template <typename T, int KIND, int V, int VPT>
+//
+// SPLIT = 2 (rows of up to 16 vectors per lane, e.g. 4096 f32): two waves
+// share a row, each holding half of it (8 vectors per lane), and combine
+// their partial sums (or maxima) through LDS; the two row units of a
+// workgroup step through their rows together, so the loop's trip count and
+// its barriers are uniform across the workgroup (rows past the end go
+// through the zero-extent descriptors like any other).
+template <typename T, int KIND, int V, int VPT, int SPLIT = 1>
 __global__ __launch_bounds__(kThreads) void rownorm_stream_kernel(RnArgs a) {
   static_assert(V > 1, "vector rows only");
+  static_assert(SPLIT == 1 || SPLIT == 2, "one or two waves per row");
+  constexpr int kUnits = kThreads / 64 / SPLIT;  // rows in flight per block
   const int lane = threadIdx.x & 63;
-  const long long gw = __builtin_amdgcn_readfirstlane(
-      blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6));
-  const long long GW = static_cast<long long>(gridDim.x) * (kThreads / 64);
+  const int wave = threadIdx.x >> 6;
+  const int unit = __builtin_amdgcn_readfirstlane(wave / SPLIT);
+  const int half = __builtin_amdgcn_readfirstlane(wave % SPLIT);
+  const int vbase = half * VPT * 64;  // first 16-byte vector of the half
+  const long long gw = static_cast<long long>(blockIdx.x) * kUnits + unit;
+  const long long GW = static_cast<long long>(gridDim.x) * kUnits;
+  __shared__ float xch[SPLIT == 2 ? 2 * 2 * (kThreads / 64) : 1];
+  // Combines a wave's partial with its partner's (SPLIT = 2): exchange
+  // slot `slot` (0 or 1, for a kind's two reductions) of row parity `par`;
+  // alternating parities keep a slot from being rewritten before the
+  // partner has read it.
+  auto combine = [&](float v, int par, int slot, bool is_max) {
+    if constexpr (SPLIT == 1) {
+      return v;
+    } else {
+      float* const x = xch + (par * 2 + slot) * (kThreads / 64);
+      if (lane == 0) x[wave] = v;
+      __syncthreads();
+      const float o = x[wave ^ 1];
+      return is_max ? fmaxf(v, o) : v + o;
+    }
+  };
   const int n = a.n;
   const int row_bytes = n * static_cast<int>(sizeof(T));
   constexpr int kNT = 2;  // nontemporal: streamed once
@@ -274,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void rownorm_stream_kernel(RnArgs a) {
     const bool bvec = (reinterpret_cast<uintptr_t>(a.beta) % 16 == 0);
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      const int base = (lane + i * 64) * V;
+      const int base = (vbase + lane + i * 64) * V;
 #pragma unroll
       for (int e = 0; e < V; ++e) {
         g[i][e] = 1.f;
@@ -299,20 +327,20 @@ __global__ __launch_bounds__(kThreads) void rownorm_stream_kernel(RnArgs a) {
     const auto rs = rsrc(a.x, row);
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
-      buf[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane + i * 64) * 16,
+      buf[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (vbase + lane + i * 64) * 16,
                                                      0, kNT);
   };
   union Pack {
     u32x4 u;
     T e[V];
   };
-  auto process = [&](long long row, const u32x4 (&buf)[VPT]) {
+  auto process = [&](long long row, const u32x4 (&buf)[VPT], int par) {
     float v[VPT][V];
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       Pack q;
       q.u = buf[i];
-      const bool in = (lane + i * 64) * V < n;
+      const bool in = (vbase + lane + i * 64) * V < n;
 #pragma unroll
       for (int e = 0; e < V; ++e)
         v[i][e] = in ? to_f32(q.e[e])
@@ -325,18 +353,21 @@ __global__ __launch_bounds__(kThreads) void rownorm_stream_kernel(RnArgs a) {
       for (int i = 0; i < VPT; ++i)
 #pragma unroll
         for (int e = 0; e < V; ++e) ss += v[i][e] * v[i][e];
-      scale = rsqrtf(wave_sum_dpp(ss) / static_cast<float>(n) + a.eps);
+      scale = rsqrtf(combine(wave_sum_dpp(ss), par, 0, false) /
+                         static_cast<float>(n) +
+                     a.eps);
     } else if constexpr (KIND == QK_ROWNORM_LAYER) {
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < VPT; ++i)
 #pragma unroll
         for (int e = 0; e < V; ++e) s += v[i][e];
-      const float mu = wave_sum_dpp(s) / static_cast<float>(n);
+      const float mu =
+          combine(wave_sum_dpp(s), par, 0, false) / static_cast<float>(n);
       float q = 0.f;
 #pragma unroll
       for (int i = 0; i < VPT; ++i) {
-        const bool in = (lane + i * 64) * V < n;
+        const bool in = (vbase + lane + i * 64) * V < n;
 #pragma unroll
         for (int e = 0; e < V; ++e) {
           const float d = in ? v[i][e] - mu : 0.f;
@@ -344,14 +375,16 @@ __global__ __launch_bounds__(kThreads) void rownorm_stream_kernel(RnArgs a) {
         }
       }
       shift = mu;
-      scale = 1.0f / sqrtf(wave_sum_dpp(q) / static_cast<float>(n) + a.eps);
+      scale = 1.0f / sqrtf(combine(wave_sum_dpp(q), par, 1, false) /
+                                static_cast<float>(n) +
+                            a.eps);
     } else {
       float mx = -INFINITY;
 #pragma unroll
       for (int i = 0; i < VPT; ++i)
 #pragma unroll
         for (int e = 0; e < V; ++e) mx = fmaxf(mx, v[i][e]);
-      mx = wave_max(mx);
+      mx = combine(wave_max(mx), par, 0, true);
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < VPT; ++i)
@@ -360,7 +393,7 @@ __global__ __launch_bounds__(kThreads) void rownorm_stream_kernel(RnArgs a) {
           v[i][e] = __expf(v[i][e] - mx);
           s += v[i][e];
         }
-      scale = 1.0f / wave_sum_dpp(s);
+      scale = 1.0f / combine(wave_sum_dpp(s), par, 1, false);
     }
     const auto rs = rsrc(a.y, row);
 #pragma unroll
@@ -374,19 +407,20 @@ __global__ __launch_bounds__(kThreads) void rownorm_stream_kernel(RnArgs a) {
         q.e[e] = from_f32<T>(o);
       }
       // Offsets at or past the row end are dropped by the descriptor.
-      __builtin_amdgcn_raw_buffer_store_b128(q.u, rs, (lane + i * 64) * 16, 0,
+      __builtin_amdgcn_raw_buffer_store_b128(q.u, rs, (vbase + lane + i * 64) * 16, 0,
                                              kNT);
     }
   };
 
   u32x4 xa[VPT], xb[VPT];
   load(gw, xa);
+  // row - unit is the same for every unit of the block (uniform trip count)
 #pragma unroll 1
-  for (long long row = gw; row < a.rows; row += 2 * GW) {
+  for (long long row = gw; row - unit < a.rows; row += 2 * GW) {
     load(row + GW, xb);
-    process(row, xa);
+    process(row, xa, 0);
     load(row + 2 * GW, xa);
-    process(row + GW, xb);
+    process(row + GW, xb, 1);
   }
 }
 
@@ -471,20 +505,25 @@ template <typename T, int KIND>
 bool LaunchStream(const RnArgs& a, hipStream_t st) {
   constexpr int V = 16 / sizeof(T);
   // Buffer descriptors take 32-bit extents; rows are at most 64 KB here.
-  auto go = [&](auto kernel) {
+  auto go = [&](auto kernel, int split = 1) {
     const int cus = DeviceComputeUnits();
+    // (1..4 workgroups per CU measured within 2% of each other at
+    // [4096, 4096].)
     const int per_cu = std::min(
         2, ResidentBlocks(reinterpret_cast<const void*>(kernel), kThreads, 0));
-    const long long waves = static_cast<long long>(per_cu) * cus *
-                            (kThreads / 64);
-    if (a.rows < 2 * waves) return false;
+    const long long units = static_cast<long long>(per_cu) * cus *
+                            (kThreads / 64 / split);
+    if (a.rows < 2 * units) return false;
     kernel<<<dim3(per_cu * cus), kThreads, 0, st>>>(a);
     return true;
   };
-  // Rows of more than 8 vectors per lane need two 16-vector buffers (one
-  // wave per SIMD); measured on MI355X the one-shot kernel is faster there.
+  // Rows of 9..16 vectors per lane: two waves per row, 8 vectors each
+  // (two 16-vector buffers per wave measured slower than the one-shot
+  // kernel).
   if (a.n <= 64 * V * 4) return go(rownorm_stream_kernel<T, KIND, V, 4>);
   if (a.n <= 64 * V * 8) return go(rownorm_stream_kernel<T, KIND, V, 8>);
+  if (a.n <= 64 * V * 16)
+    return go(rownorm_stream_kernel<T, KIND, V, 8, 2>, 2);
   return false;
 }
 
