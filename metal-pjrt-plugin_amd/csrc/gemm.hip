@@ -272,18 +272,18 @@ qk_status DispatchTile(const GemmArgs& g, int batch, bool ta, bool tb,
   return PostLaunch(name);
 }
 
-template <typename T, int BN>
+template <typename T, int BN, int NW = 4>
 qk_status DispatchFast(const GemmArgs& g, int batch, bool ta, bool tb,
                        hipStream_t stream, const char* name) {
   dim3 grid(g.tiles_m * g.tiles_n, batch);
   if (!ta && !tb)
-    gemm_dma_kernel<T, BN, false, false><<<grid, 256, 0, stream>>>(g);
+    gemm_dma_kernel<T, BN, false, false, NW><<<grid, NW * 64, 0, stream>>>(g);
   else if (!ta && tb)
-    gemm_dma_kernel<T, BN, false, true><<<grid, 256, 0, stream>>>(g);
+    gemm_dma_kernel<T, BN, false, true, NW><<<grid, NW * 64, 0, stream>>>(g);
   else if (ta && !tb)
-    gemm_dma_kernel<T, BN, true, false><<<grid, 256, 0, stream>>>(g);
+    gemm_dma_kernel<T, BN, true, false, NW><<<grid, NW * 64, 0, stream>>>(g);
   else
-    gemm_dma_kernel<T, BN, true, true><<<grid, 256, 0, stream>>>(g);
+    gemm_dma_kernel<T, BN, true, true, NW><<<grid, NW * 64, 0, stream>>>(g);
   return PostLaunch(name);
 }
 
@@ -346,11 +346,12 @@ constexpr HalfTile kHalfTiles[] = {
     {64, 64, 2, 2},    // 3
     {256, 128, 2, 2},  // 4
     {128, 256, 2, 2},  // 5
-    {256, 256, 2, 2},  // 6: interior-tile LDS-DMA kernel (gemm_dma_kernel)
+    {256, 256, 4, 2},  // 6: interior-tile LDS-DMA kernel (gemm_dma_kernel),
+                       //    8 waves of 64 x 128, two per SIMD
     {256, 128, 2, 2},  // 7: interior-tile LDS-DMA kernel, 128 x 64 per wave
     {64, 64, 2, 2},    // 8: split-K, four waves each a quarter of K
     {32, 32, 2, 4},    // 9: split-K for up to 32 rows, eight waves
-    {256, 192, 2, 2},  // 10: interior-tile LDS-DMA kernel, 128 x 96 per wave
+    {256, 192, 4, 2},  // 10: interior-tile LDS-DMA kernel, 8 waves of 64 x 96
 };
 constexpr int kFastTile256 = 6, kFastTile128 = 7, kSplitK = 8, kSplitK32 = 9,
               kFastTile192 = 10;
@@ -478,11 +479,11 @@ qk_status DispatchHalf(int tile, const GemmArgs& g, int batch, bool ta,
     case 5:
       return DispatchTile<T, 128, 256, 64, 2, 2>(g, batch, ta, tb, st, name);
     case kFastTile256:
-      return DispatchFast<T, 256>(g, batch, ta, tb, st, name);
+      return DispatchFast<T, 256, 8>(g, batch, ta, tb, st, name);
     case kFastTile128:
       return DispatchFast<T, 128>(g, batch, ta, tb, st, name);
     case kFastTile192:
-      return DispatchFast<T, 192>(g, batch, ta, tb, st, name);
+      return DispatchFast<T, 192, 8>(g, batch, ta, tb, st, name);
     case kSplitK:
       return DispatchSplitK<T, 64, 4>(g, batch, ta, tb, st, name);
     case kSplitK32:

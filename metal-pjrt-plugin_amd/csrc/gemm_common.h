@@ -542,43 +542,39 @@ __device__ __forceinline__ void store_direct_t(
   const O* C = static_cast<const O*>(g.c);
   O* aux = static_cast<O*>(g.aux);
   O* D = static_cast<O*>(g.d);
-  // One block row (i) at a time; each optional term is one uniform branch
-  // around a loop over the block row's FN x 16 values.
+  // One 32x32 block at a time (16 values per lane, few registers beyond
+  // the accumulators); each optional term is one uniform branch around a
+  // loop over the block's 16 values.
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    float v[FN][16];
-    long long rb[16];
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-      rb[r] = dbase + static_cast<long long>(rowb + i * 32 + 8 * (r >> 2) + (r & 3)) * g.ldd + colb;
+    for (int j = 0; j < FN; ++j) {
+      const long long base =
+          dbase + static_cast<long long>(rowb + i * 32) * g.ldd + colb +
+          j * 32;
+      auto at = [&](int r) {
+        return base + static_cast<long long>(8 * (r >> 2) + (r & 3)) * g.ldd;
+      };
+      float v[16];
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+      for (int r = 0; r < 16; ++r) v[r] = g.alpha * acc[i][j][r];
+      if (g.use_c) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) v[j][r] = g.alpha * acc[i][j][r];
-    if (g.use_c) {
+        for (int r = 0; r < 16; ++r) v[r] += g.beta * to_f32(C[at(r)]);
+      }
+      if (g.has_bias) {
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
+        for (int r = 0; r < 16; ++r) v[r] += bias[j];
+      }
+      if (g.has_aux) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) v[j][r] += g.beta * to_f32(C[rb[r] + j * 32]);
+        for (int r = 0; r < 16; ++r) aux[at(r)] = from_f32<O>(v[r]);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) D[at(r)] = from_f32<O>(act_f32(ACT, v[r]));
     }
-    if (g.has_bias) {
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[j][r] += bias[j];
-    }
-    if (g.has_aux) {
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) aux[rb[r] + j * 32] = from_f32<O>(v[j][r]);
-    }
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) D[rb[r] + j * 32] = from_f32<O>(act_f32(ACT, v[j][r]));
-  }
 }
+
 template <typename T, int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_direct(
     const GemmArgs& g, const f32x16 (&acc)[BM / WM / 32][BN / WN / 32],

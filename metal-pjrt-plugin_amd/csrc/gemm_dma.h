@@ -72,9 +72,9 @@ struct DmaRsrc {
 // Operand tile of R rows x 64 K, K-contiguous in memory (row stride ld
 // elements): R / 32 DMA instructions per wave; instruction i of wave w
 // fills rows (4 i + w) * 8 .. + 8.
-template <typename T, int R>
+template <typename T, int R, int NW = 4>
 struct DmaK {
-  static constexpr int NI = R / 32;
+  static constexpr int NI = R / (8 * NW);
   static constexpr int kBytes = R * 128;
   DmaRsrc rs;
   int voff, ld;
@@ -87,8 +87,8 @@ struct DmaK {
   }
   __device__ __forceinline__ void issue(unsigned char* lds, int r0, int k0,
                                         int w, int i) const {
-    rs.dma(lds + (i * 4 + w) * 1024, voff,
-           ((r0 + i * 32) * ld + k0) * static_cast<int>(sizeof(T)));
+    rs.dma(lds + (i * NW + w) * 1024, voff,
+           ((r0 + i * 8 * NW) * ld + k0) * static_cast<int>(sizeof(T)));
   }
   // Fragment for rows rb .. rb + 31 (rb % 32 == 0), K elements kb + 8 (lane
   // / 32) .. + 7.
@@ -105,12 +105,12 @@ struct DmaK {
 // stride ld elements): K row k occupies R * sizeof(T) bytes; a DMA
 // instruction covers RPI K rows, instruction i of wave w fills K rows
 // (4 i + w) * RPI .. + RPI.
-template <typename T, int R>
+template <typename T, int R, int NW = 4>
 struct DmaMN {
   static constexpr int RB = R * static_cast<int>(sizeof(T));  // row bytes
   static constexpr int LPR = RB / 16;                         // lanes per row
   static constexpr int RPI = 64 / LPR;  // K rows per instruction
-  static constexpr int NI = 64 / RPI / 4;
+  static constexpr int NI = 64 / RPI / NW;
   static constexpr int kBytes = 64 * RB;
   static_assert(LPR >= 8 && 64 % LPR == 0, "row must span 8..64 chunks");
   DmaRsrc rs;
@@ -120,13 +120,14 @@ struct DmaMN {
     rs.make(src, bytes);
     ld = ld_;
     const int k = w * RPI + lane / LPR;  // k & 3 is the same for every i
+    static_assert((NW * RPI) % 4 == 0, "swizzle phase per instruction");
     voff = (k * ld + ((lane % LPR) ^ ((k & 3) << 1)) * 8) *
            static_cast<int>(sizeof(T));
   }
   __device__ __forceinline__ void issue(unsigned char* lds, int r0, int k0,
                                         int w, int i) const {
-    rs.dma(lds + (i * 4 + w) * 1024, voff,
-           ((k0 + i * 4 * RPI) * ld + r0) * static_cast<int>(sizeof(T)));
+    rs.dma(lds + (i * NW + w) * 1024, voff,
+           ((k0 + i * NW * RPI) * ld + r0) * static_cast<int>(sizeof(T)));
   }
   // Fragment for columns rb .. rb + 31 and K kb .. kb + 15 with the
   // transposing read (lane s of a 16-lane group addresses K row
@@ -148,10 +149,10 @@ struct DmaMN {
 // A 192-column M/N-contiguous tile as two DmaMN regions, columns 0..127
 // (256-byte K rows) and 128..191 (128-byte K rows): 4 + 2 DMA instructions
 // per wave. Every 32-column fragment lies in one region.
-template <typename T>
+template <typename T, int NW = 4>
 struct DmaMN192 {
-  using Lo = DmaMN<T, 128>;
-  using Hi = DmaMN<T, 64>;
+  using Lo = DmaMN<T, 128, NW>;
+  using Hi = DmaMN<T, 64, NW>;
   static constexpr int NI = Lo::NI + Hi::NI;
   static constexpr int kBytes = Lo::kBytes + Hi::kBytes;
   Lo lo;
@@ -191,14 +192,14 @@ constexpr int VmcntImm(int n) {
   return (n & 0xF) | (((n >> 4) & 3) << 14) | (7 << 4) | (0xF << 8);
 }
 
-template <typename T, int BN, bool TA, bool TB>
-__global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs g) {
-  constexpr int BM = 256, BK = 64, WM = 2, WN = 2;
+template <typename T, int BN, bool TA, bool TB, int NWV = 4>
+__global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(GemmArgs g) {
+  constexpr int BM = 256, BK = 64, WN = 2, WM = NWV / WN;
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
-  using LA = std::conditional_t<TA, DmaMN<T, BM>, DmaK<T, BM>>;
+  using LA = std::conditional_t<TA, DmaMN<T, BM, NWV>, DmaK<T, BM, NWV>>;
   using LB = std::conditional_t<
-      TB, DmaK<T, BN>,
-      std::conditional_t<BN == 192, DmaMN192<T>, DmaMN<T, BN>>>;
+      TB, DmaK<T, BN, NWV>,
+      std::conditional_t<BN == 192, DmaMN192<T, NWV>, DmaMN<T, BN, NWV>>>;
   constexpr int kBOff = LA::kBytes;
   constexpr int kStage = LA::kBytes + LB::kBytes;
   constexpr int kDma = LA::NI + LB::NI;  // DMA instructions per wave per tile
