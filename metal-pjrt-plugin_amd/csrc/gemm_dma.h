@@ -43,32 +43,6 @@
 namespace qk {
 namespace {
 
-// Raw buffer descriptor in SGPRs (base, extent in bytes, raw access).
-struct DmaRsrc {
-  u32x4 d;
-  __device__ __forceinline__ void make(const void* p, long long bytes) {
-    const unsigned long long a = reinterpret_cast<unsigned long long>(p);
-    d[0] = static_cast<uint32_t>(a);
-    d[1] = static_cast<uint32_t>(a >> 32) & 0xFFFFu;
-    d[2] = static_cast<uint32_t>(bytes);
-    d[3] = 0x00020000u;
-  }
-  // One 16-byte-per-lane DMA into lds[0..1024): lane L's 16 bytes from
-  // byte voff + soff of the buffer land at lds + 16 L.
-  __device__ __forceinline__ void dma(unsigned char* lds, int voff,
-                                      int soff) const {
-    // LDS byte address (an address-space cast, then the 32-bit value).
-    using LdsPtr = __attribute__((address_space(3))) unsigned char*;
-    const uint32_t base =
-        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsPtr)lds));
-    asm volatile(
-        "s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-        :
-        : "v"(voff), "s"(d), "s"(soff), "s"(base)
-        : "memory", "m0");
-  }
-};
-
 // Operand tile of R rows x 64 K, K-contiguous in memory (row stride ld
 // elements): R / 32 DMA instructions per wave; instruction i of wave w
 // fills rows (4 i + w) * 8 .. + 8.

@@ -1,5 +1,5 @@
 // Device-side helpers shared by the gfx950 kernels: element conversion,
-// activations and wavefront reductions.
+// activations, wavefront reductions and LDS DMA.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -150,6 +150,91 @@ __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
   return v;
+}
+
+// LDS DMA (buffer_load ... lds) of 16 or 4 bytes per lane into
+// lds + lane * size, as device-only helpers (the address-space cast of the
+// LDS pointer is not valid host code). The Nt form reads nontemporally
+// (data streamed once).
+using LdsPtr = __attribute__((address_space(3))) void*;
+__device__ __forceinline__ void DmaLds16(__amdgpu_buffer_rsrc_t r,
+                                         unsigned char* lds, int voff,
+                                         int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)lds, 16, voff, soff, 0,
+                                           0);
+}
+__device__ __forceinline__ void DmaLds16Nt(__amdgpu_buffer_rsrc_t r,
+                                           unsigned char* lds, int voff,
+                                           int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)lds, 16, voff, soff, 0,
+                                           2);
+}
+__device__ __forceinline__ void DmaLds4(__amdgpu_buffer_rsrc_t r,
+                                        unsigned char* lds, int voff,
+                                        int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)lds, 4, voff, soff, 0,
+                                           0);
+}
+
+// Raw buffer descriptor in SGPRs (base, extent in bytes, raw access) whose
+// LDS DMA is issued as inline asm: the compiler's wait-count pass does not
+// see it, so it adds no waits of its own for it (it would otherwise make
+// LDS reads it cannot tell apart from the DMA's destination wait for every
+// DMA in flight); the caller waits explicitly (s_waitcnt vmcnt) before
+// reading what a DMA wrote. Lane L's bytes from byte voff + soff of the
+// buffer land at lds + L * size.
+struct DmaRsrc {
+  uint32_t d __attribute__((ext_vector_type(4)));
+  __device__ __forceinline__ void make(const void* p, long long bytes) {
+    const unsigned long long a = reinterpret_cast<unsigned long long>(p);
+    d[0] = static_cast<uint32_t>(a);
+    d[1] = static_cast<uint32_t>(a >> 32) & 0xFFFFu;
+    d[2] = static_cast<uint32_t>(bytes);
+    d[3] = 0x00020000u;
+  }
+  static __device__ __forceinline__ uint32_t lds_addr(unsigned char* lds) {
+    using LdsBytes = __attribute__((address_space(3))) unsigned char*;
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsBytes)lds));
+  }
+  // 16 bytes per lane.
+  __device__ __forceinline__ void dma(unsigned char* lds, int voff,
+                                      int soff) const {
+    asm volatile(
+        "s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+        :
+        : "v"(voff), "s"(d), "s"(soff), "s"(lds_addr(lds))
+        : "memory", "m0");
+  }
+  // 16 bytes per lane, nontemporal (data streamed once).
+  __device__ __forceinline__ void dma_nt(unsigned char* lds, int voff,
+                                         int soff) const {
+    asm volatile(
+        "s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen nt lds"
+        :
+        : "v"(voff), "s"(d), "s"(soff), "s"(lds_addr(lds))
+        : "memory", "m0");
+  }
+  // 4 bytes per lane.
+  __device__ __forceinline__ void dma4(unsigned char* lds, int voff,
+                                       int soff) const {
+    asm volatile(
+        "s_mov_b32 m0, %3\n\tbuffer_load_dword %0, %1, %2 offen lds"
+        :
+        : "v"(voff), "s"(d), "s"(soff), "s"(lds_addr(lds))
+        : "memory", "m0");
+  }
+};
+
+// Volatile 32-bit LDS accesses (flags polled by other waves of the
+// workgroup) through an LDS-typed pointer: as generic pointers they would
+// become flat accesses, which count in the memory counter too.
+__device__ __forceinline__ uint32_t LdsLoadVolatile(const uint32_t* p) {
+  using P = const volatile __attribute__((address_space(3))) uint32_t*;
+  return *(P)p;
+}
+__device__ __forceinline__ void LdsStoreVolatile(uint32_t* p, uint32_t v) {
+  using P = volatile __attribute__((address_space(3))) uint32_t*;
+  *(P)p = v;
 }
 
 }  // namespace qk

@@ -71,27 +71,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t Rsrc(const void* p,
                                            bytes, 0x00020000);
 }
 
-// LDS DMA of 16 or 4 bytes per lane into lds + lane * size, as device-only
-// helpers (the address-space cast of the LDS pointer is not valid host
-// code). Dma16Nt reads nontemporally (streamed once).
-using LdsPtr = __attribute__((address_space(3))) void*;
-__device__ __forceinline__ void Dma16(__amdgpu_buffer_rsrc_t r,
-                                      unsigned char* lds, int voff, int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)lds, 16, voff, soff, 0,
-                                           0);
-}
-__device__ __forceinline__ void Dma16Nt(__amdgpu_buffer_rsrc_t r,
-                                        unsigned char* lds, int voff,
-                                        int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)lds, 16, voff, soff, 0,
-                                           kNonTemporal);
-}
-__device__ __forceinline__ void Dma4(__amdgpu_buffer_rsrc_t r,
-                                     unsigned char* lds, int voff, int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)lds, 4, voff, soff, 0,
-                                           0);
-}
-
 // Eight codes -> bf16(q * s + b). int4: the 8 nibbles of a u32x8 word, code
 // j at bits 4 j; int8: 8 bytes (s8: signed).
 template <int PACK>
@@ -183,13 +162,13 @@ __global__ __launch_bounds__(KW * 64) void qmm_mid_kernel(MdArgs a) {
     const int g = g0 + min(gi, a.gpw - 1);
 #pragma unroll
     for (int i = 0; i < kCDma; ++i)
-      Dma16Nt(crs, slot + kCOff + i * 1024, cvo[i] + oob,
+      DmaLds16Nt(crs, slot + kCOff + i * 1024, cvo[i] + oob,
                             g * GB);
-    Dma4(srs, slot + kSOff, svo + oob, (g & ~1) * 2);
-    Dma4(brs, slot + kBOff, svo + oob, (g & ~1) * 2);
+    DmaLds4(srs, slot + kSOff, svo + oob, (g & ~1) * 2);
+    DmaLds4(brs, slot + kBOff, svo + oob, (g & ~1) * 2);
 #pragma unroll
     for (int i = 0; i < TM / 8; ++i)
-      Dma16(xrs, slot + kXOff + i * 1024, xvo + i * 8 * a.k * 2 + oob,
+      DmaLds16(xrs, slot + kXOff + i * 1024, xvo + i * 8 * a.k * 2 + oob,
                  g * 128);
   };
 

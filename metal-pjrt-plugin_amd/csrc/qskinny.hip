@@ -44,6 +44,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdlib>
+#include <type_traits>
 
 #include "qk_device.h"
 #include "qk_internal.h"
@@ -251,6 +252,35 @@ __global__ __launch_bounds__(KW * 64) void qmm_skinny_kernel(SkArgs a) {
     for (int i = 0; i < XL; ++i)
       *reinterpret_cast<u32x4*>(x_buf + (XRPL * i + lane / XLPR) * kXRow +
                                 16 * (lane % XLPR)) = t.x[i];
+    // Every LDS read of the sub-chunk is issued before any of it is used:
+    // one LDS round trip per sub-chunk instead of one per group and row
+    // block.
+    u32x4 xv[CG][MB][2];
+#pragma unroll
+    for (int gg = 0; gg < CG; ++gg)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+          xv[gg][mb][t2] = *reinterpret_cast<const u32x4*>(
+              x_buf + (16 * mb + l16) * kXRow + gg * 128 + 32 * q16 + 16 * t2);
+    using CodeT = typename std::conditional<kInt4, u32x2, u32x4>::type;
+    CodeT wv[CG][NB];
+    uint32_t sv[NB][CG / 2], bv[NB][CG / 2];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int row = 16 * nb + l16;
+#pragma unroll
+      for (int gg = 0; gg < CG; ++gg)
+        wv[gg][nb] = *reinterpret_cast<const CodeT*>(
+            code_buf + row * kRow + gg * GB + (kInt4 ? 8 : 16) * q16);
+#pragma unroll
+      for (int h = 0; h < CG / 2; ++h) {
+        sv[nb][h] = reinterpret_cast<const uint32_t*>(sb_buf + row * CG)[h];
+        bv[nb][h] =
+            reinterpret_cast<const uint32_t*>(sb_buf + (NR + row) * CG)[h];
+      }
+    }
 #pragma unroll
     for (int gg = 0; gg < CG; ++gg) {
       bf16x8 xa[MB][2];
@@ -261,33 +291,25 @@ __global__ __launch_bounds__(KW * 64) void qmm_skinny_kernel(SkArgs a) {
 #pragma unroll
         for (int t2 = 0; t2 < 2; ++t2) {
           // int4: x in the pair order of the code words; int8: as loaded
-          const u32x4 xv = *reinterpret_cast<const u32x4*>(
-              x_buf + (16 * mb + l16) * kXRow + gg * 128 + 32 * q16 +
-              16 * t2);
-          xa[mb][t2] = kInt4 ? XPairs(xv) : __builtin_bit_cast(bf16x8, xv);
+          xa[mb][t2] = kInt4 ? XPairs(xv[gg][mb][t2])
+                             : __builtin_bit_cast(bf16x8, xv[gg][mb][t2]);
           xs[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[mb][t2], ones,
                                                            xs[mb], 0, 0, 0);
         }
       }
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const int row = 16 * nb + l16;
         bf16x8 b0, b1;
         if constexpr (kInt4) {
-          const u32x2 w = *reinterpret_cast<const u32x2*>(
-              code_buf + row * kRow + gg * GB + 8 * q16);
-          b0 = CodePairs(w[0], kMask, kBias);
-          b1 = CodePairs(w[1], kMask, kBias);
+          b0 = CodePairs(wv[gg][nb][0], kMask, kBias);
+          b1 = CodePairs(wv[gg][nb][1], kMask, kBias);
         } else {
-          const u32x4 w = *reinterpret_cast<const u32x4*>(
-              code_buf + row * kRow + gg * GB + 16 * q16);
-          b0 = CodeBytes<PACK>(w[0], w[1]);
-          b1 = CodeBytes<PACK>(w[2], w[3]);
+          b0 = CodeBytes<PACK>(wv[gg][nb][0], wv[gg][nb][1]);
+          b1 = CodeBytes<PACK>(wv[gg][nb][2], wv[gg][nb][3]);
         }
-        const float sc = __uint_as_float(
-            static_cast<uint32_t>(sb_buf[row * CG + gg]) << 16);
-        const float of = __uint_as_float(
-            static_cast<uint32_t>(sb_buf[(NR + row) * CG + gg]) << 16);
+        const int sh = 16 * (gg & 1);
+        const float sc = __uint_as_float((sv[nb][gg >> 1] >> sh) << 16);
+        const float of = __uint_as_float((bv[nb][gg >> 1] >> sh) << 16);
         // int4 and signed int8 codes enter as q + 128
         const float off = PACK == QK_PACK_U8 ? of : of - 128.f * sc;
 #pragma unroll
@@ -351,6 +373,256 @@ auto Skinny8() {
     return static_cast<K>(nullptr);
 }
 
+// The streamed form for one block of 16 rows of x (M <= 16) and int4
+// (u32x8) codes, with the loads and the arithmetic in different waves.
+// A workgroup owns NR = 16 NB weight rows and all of K, cut into items of
+// four groups (K = 256): x (16 rows x 512 bytes), codes (NR rows x 128
+// bytes) and scale / offset dwords.
+//  - Two producer waves move items (the even and the odd ones) from
+//    global memory into a ring of S slots in LDS by LDS DMA, each with up
+//    to three items in flight (the most the memory counter of one wave,
+//    63 instructions, can tell apart). A producer never computes, so the
+//    memory queue stays full.
+//  - NC consumer waves (consumer c takes items c, c + NC, ...) read the
+//    items from LDS and compute. A consumer never issues a global load,
+//    so it never stalls behind a full memory queue.
+//  - Hand-off through LDS words: ready[s] = j + 1 once item j has landed
+//    in slot s = j % S, freed[s] = j + 1 once its consumer has read it.
+//    Every wait is a bounded spin (the kernel ends even if a flag never
+//    comes).
+// The arithmetic is that of qmm_skinny_kernel with MB = 1; the consumers'
+// partial tiles are summed through LDS at the end. Measured against the
+// register-staged kernel at M = 16: 12288 x 4096 11.8 vs 12.5 us, 4096 x
+// 12288 13.6 vs 14.7 us; it is used when every workgroup fits on the GPU
+// at once (the lm_head's 3166 row blocks run faster on the register-staged
+// kernel, whose workgroups overlap one another).
+template <int NB>
+constexpr int WsSlotBytes() {
+  // x, codes (whole 1 KB DMA instructions), scales and offsets (two dwords
+  // per row, whole 256-byte instructions)
+  return 8192 + ((128 * 16 * NB + 1023) / 1024) * 1024 +
+         2 * ((32 * NB + 63) / 64) * 256;
+}
+constexpr int kWsConsumers = 8, kWsProducers = 2;
+
+template <int NB>
+__global__ __launch_bounds__((kWsConsumers + kWsProducers) * 64) void
+qmm_ws_kernel(SkArgs a) {
+  constexpr int NC = kWsConsumers, NP = kWsProducers;
+  constexpr int NR = 16 * NB;                  // weight rows per workgroup
+  constexpr int TS = NR + 1;                   // partial-tile row stride
+  constexpr int kCDma = (NR * 128 + 1023) / 1024;
+  constexpr int kSDma = (NR * 2 + 63) / 64;
+  constexpr int kCOff = 8192, kSOff = kCOff + kCDma * 1024,
+                kBOff = kSOff + kSDma * 256;
+  constexpr int kSlot = WsSlotBytes<NB>();
+  constexpr int kDma = 8 + kCDma + 2 * kSDma;  // DMA instructions per item
+  constexpr int kFly = 3;                      // items in flight / producer
+  constexpr int S = (150 * 1024) / kSlot;      // ring slots
+  static_assert(kBOff + kSDma * 256 == kSlot, "slot layout");
+  static_assert(kFly * kDma <= 63, "memory counter");
+  static_assert(S >= NP * kFly + 1, "ring depth");
+  static_assert(S * kSlot >= NC * 16 * TS * 4, "partial tiles fit");
+  __shared__ __attribute__((aligned(16))) unsigned char ring[S * kSlot];
+  __shared__ uint32_t flags[2 * S];  // ready[S], freed[S]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * NR;
+  const int G = a.groups;
+  const int items = G / 4;
+  uint32_t* const ready = flags;
+  uint32_t* const freed = flags + S;
+  if (threadIdx.x < 2 * S) LdsStoreVolatile(flags + threadIdx.x, 0);
+  __syncthreads();
+
+  // A spin of at most 2^20 polls (~70 ms): a wave that waits longer gives
+  // up and goes on (wrong results, but the kernel ends).
+  auto spin_until = [](const uint32_t* f, uint32_t want) {
+    for (int it = 0; it < (1 << 20); ++it) {
+      if (__builtin_amdgcn_readfirstlane(LdsLoadVolatile(f)) == want) return;
+      __builtin_amdgcn_s_sleep(1);
+    }
+  };
+
+  f32x4 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (wave >= NC) {
+    // Producer p = wave - NC moves items p, p + NP, ... Lane maps (each
+    // DMA writes 16 or 4 bytes per lane at lane * size of its destination;
+    // rows past M / N read zeros); 16-byte chunk j of each 128-byte group
+    // of a row is stored in place j ^ sw(row), so that the rows of one
+    // fragment read fall in distinct banks:
+    //  x: 2 rows of 512 bytes per instruction, sw(r) = r & 7;
+    //  codes: 8 rows of 128 bytes per instruction, sw(r) = (r / 2) & 7;
+    //  scales / offsets: lane L, row n0 + L / 2, dword L % 2 (groups
+    //    4 j + 2 (L % 2) and 4 j + 2 (L % 2) + 1).
+    const int p = wave - NC;
+    const int row_bytes = a.k / 2;
+    DmaRsrc crs, xrs, srs, brs;
+    crs.make(a.codes, static_cast<long long>(a.n) * row_bytes);
+    xrs.make(a.x, static_cast<long long>(a.m) * a.k * 2);
+    srs.make(a.scales, static_cast<long long>(a.n) * G * 2);
+    brs.make(a.biases, a.has_bias ? static_cast<long long>(a.n) * G * 2 : 0);
+    int xvo[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 2 * i + lane / 32, q = lane % 32;
+      xvo[i] = (r * a.k + ((q & ~7) | ((q & 7) ^ (r & 7))) * 8) * 2;
+    }
+    int cvo[kCDma];
+#pragma unroll
+    for (int i = 0; i < kCDma; ++i) {
+      const int rr = 8 * i + lane / 8, q = lane % 8;
+      const int r = n0 + rr;
+      cvo[i] = (rr < NR && r < a.n)
+                   ? r * row_bytes + ((q ^ ((rr >> 1) & 7)) << 4)
+                   : kOut;
+    }
+    int svo[kSDma];
+#pragma unroll
+    for (int i = 0; i < kSDma; ++i) {
+      const int rr = (64 * i + lane) / 2;
+      svo[i] = (rr < NR && n0 + rr < a.n)
+                   ? (n0 + rr) * G * 2 + ((64 * i + lane) % 2) * 4
+                   : kOut;
+    }
+    auto publish = [&](int j) {
+      if (lane == 0) LdsStoreVolatile(ready + j % S, j + 1);
+    };
+    int issued = 0, published = 0;  // own items
+    for (int j = p; j < items; j += NP) {
+      const int s = j % S;
+      unsigned char* slot = ring + s * kSlot;
+      if (j >= S && __builtin_amdgcn_readfirstlane(LdsLoadVolatile(
+                        freed + s)) != static_cast<uint32_t>(j - S + 1)) {
+        // Publish everything in flight before waiting: a consumer of one
+        // of those items may be what frees the slot.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        for (; published < issued; ++published) publish(p + NP * published);
+        spin_until(freed + s, j - S + 1);
+      }
+      const int g = 4 * j;
+#pragma unroll
+      for (int i = 0; i < kCDma; ++i)
+        crs.dma_nt(slot + kCOff + i * 1024, cvo[i], g * 32);
+#pragma unroll
+      for (int i = 0; i < kSDma; ++i) {
+        srs.dma4(slot + kSOff + i * 256, svo[i], g * 2);
+        brs.dma4(slot + kBOff + i * 256, svo[i], g * 2);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xrs.dma(slot + i * 1024, xvo[i], g * 128);
+      ++issued;
+      if (issued - published >= kFly) {
+        // the oldest own item in flight has landed once at most kFly - 1
+        // later ones are outstanding
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kFly - 1) * kDma)
+                     : "memory");
+        publish(p + NP * published);
+        ++published;
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    for (; published < issued; ++published) publish(p + NP * published);
+  } else {
+    const int q16 = lane >> 4, l16 = lane & 15;
+    const uint32_t kMask = vgpr_const(0x000F000Fu);
+    const uint32_t kBias = vgpr_const(0x43004300u);
+    const bf16x8 ones = __builtin_bit_cast(
+        bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+    for (int j = wave; j < items; j += NC) {
+      const int s = j % S;
+      const unsigned char* slot = ring + s * kSlot;
+      spin_until(ready + s, j + 1);
+      asm volatile("" ::: "memory");  // the slot's reads stay below
+      // The item's operands in one LDS round trip: per group, the lane's
+      // x chunks 2 (l / 16) and 2 (l / 16) + 1 of row l % 16, its code
+      // words 2 (l / 16) and 2 (l / 16) + 1 of each row block, and the
+      // group's scale and offset of each row block.
+      u32x4 xv[4][2];
+      u32x2 wv[4][NB];
+      uint32_t sv[2][NB], bv[2][NB];
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          xv[gg][h] = *reinterpret_cast<const u32x4*>(
+              slot + l16 * 512 +
+              ((8 * gg + ((2 * q16 + h) ^ (l16 & 7))) << 4));
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int r = 16 * nb + l16;
+          const int c = 2 * gg + (q16 >> 1);
+          wv[gg][nb] = *reinterpret_cast<const u32x2*>(
+              slot + kCOff + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) +
+              ((q16 & 1) << 3));
+        }
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int r = 16 * nb + l16;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          sv[h][nb] =
+              *reinterpret_cast<const uint32_t*>(slot + kSOff + r * 8 + 4 * h);
+          bv[h][nb] =
+              *reinterpret_cast<const uint32_t*>(slot + kBOff + r * 8 + 4 * h);
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (lane == 0) LdsStoreVolatile(freed + s, j + 1);
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg) {
+        const bf16x8 x0 = XPairs(xv[gg][0]), x1 = XPairs(xv[gg][1]);
+        f32x4 xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            x0, ones, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, ones, xs, 0, 0, 0);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              x0, CodePairs(wv[gg][nb][0], kMask, kBias),
+              f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              x1, CodePairs(wv[gg][nb][1], kMask, kBias), tmp, 0, 0, 0);
+          const int sh = 16 * (gg & 1);
+          const float sc = __uint_as_float((sv[gg >> 1][nb] >> sh) << 16);
+          const float of = __uint_as_float((bv[gg >> 1][nb] >> sh) << 16);
+          const float off = of - 128.f * sc;  // codes enter as q + 128
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[nb][r] = fmaf(sc, tmp[r], fmaf(off, xs[r], acc[nb][r]));
+        }
+      }
+    }
+  }
+
+  // Sum the consumers' partial tiles (the ring is idle: every DMA has
+  // landed and been read) and store rows < M, columns < N.
+  __syncthreads();
+  float* const part = reinterpret_cast<float*>(ring);
+  if (wave < NC) {
+    const int q16 = lane >> 4, l16 = lane & 15;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        part[(wave * 16 + 4 * q16 + r) * TS + 16 * nb + l16] = acc[nb][r];
+  }
+  __syncthreads();
+  bf16* Y = static_cast<bf16*>(a.y);
+  for (int e = threadIdx.x; e < 16 * NR; e += (NC + NP) * 64) {
+    const int r = e / NR, c = e % NR;
+    if (r >= a.m || n0 + c >= a.n) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NC; ++w) v += part[(w * 16 + r) * TS + c];
+    Y[static_cast<long long>(r) * a.n + n0 + c] = from_f32<bf16>(v);
+  }
+}
+
 }  // namespace
 
 bool QSkinnyApplies(const QuantProblem& p) {
@@ -390,6 +662,29 @@ qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream) {
   // CU one (16 for more than 32 rows of x); eight waves split K (fewer
   // when K is short), each walking k / KW.
   const bool int4 = p.packing == QK_PACK_U32X8;
+  // QK_SKINNY_WS=0 turns the streamed kernel off (tuning).
+  static const bool ws_off = [] {
+    const char* v = std::getenv("QK_SKINNY_WS");
+    return v != nullptr && *v == '0';
+  }();
+  // The streamed kernel when all of its workgroups are resident at once:
+  // 16, 32 or 48 weight rows each, the fewest for which one workgroup per
+  // CU covers N.
+  const int ws_nb = (a.n + 15) / 16 <= cus   ? 1
+                    : (a.n + 31) / 32 <= cus ? 2
+                    : (a.n + 47) / 48 <= cus ? 3
+                                             : 0;
+  if (int4 && mb == 1 && !ws_off && a.groups % 4 == 0 && ws_nb > 0) {
+    const int grid = (a.n + 16 * ws_nb - 1) / (16 * ws_nb);
+    constexpr int threads = (kWsConsumers + kWsProducers) * 64;
+    if (ws_nb == 3)
+      qmm_ws_kernel<3><<<grid, threads, 0, stream>>>(a);
+    else if (ws_nb == 2)
+      qmm_ws_kernel<2><<<grid, threads, 0, stream>>>(a);
+    else
+      qmm_ws_kernel<1><<<grid, threads, 0, stream>>>(a);
+    return PostLaunch("qmm_ws");
+  }
   const int cg = int4 && mb <= 2 ? 4 : 2;
   bool wide = (a.n + 31) / 32 >= cus && mb <= (int4 ? 2 : 1);
   // QK_SKINNY_ROWS=16|32 forces the weight rows per workgroup (tuning).
@@ -399,7 +694,12 @@ qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream) {
   }();
   if (forced_rows == 16) wide = false;
   if (forced_rows == 32 && mb <= (int4 ? 2 : 1)) wide = true;
-  const int nr = wide ? 32 : 16;
+  // 48 weight rows per workgroup (three row blocks) when that still gives
+  // every CU one: x is read once per workgroup, so fewer, taller
+  // workgroups read less of it.
+  const bool tall = int4 && mb == 1 && (forced_rows == 48 ||
+                    (forced_rows == 0 && a.n / 48 >= cus));
+  const int nr = tall ? 48 : wide ? 32 : 16;
   const dim3 grid((a.n + nr - 1) / nr);
   // The most waves per workgroup (8, 4 or 2) for which every workgroup is
   // resident at once (no second, partly empty round) and k splits evenly.
@@ -429,7 +729,8 @@ qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream) {
   if (p.packing == QK_PACK_U32X8) {
     switch (mb) {
       case 1:
-        if (wide) QK_SKINNY(QK_PACK_U32X8, 1, 2, 4);
+        if (tall) QK_SKINNY(QK_PACK_U32X8, 1, 3, 4);
+        else if (wide) QK_SKINNY(QK_PACK_U32X8, 1, 2, 4);
         else QK_SKINNY(QK_PACK_U32X8, 1, 1, 4);
         break;
       case 2:
