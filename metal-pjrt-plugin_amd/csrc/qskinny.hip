@@ -374,14 +374,14 @@ auto Skinny8() {
 }
 
 // The streamed form for one block of 16 rows of x (M <= 16) and int4
-// (u32x8) codes, with the loads and the arithmetic in different waves.
-// A workgroup owns NR = 16 NB weight rows and all of K, cut into items of
-// four groups (K = 256): x (16 rows x 512 bytes), codes (NR rows x 128
-// bytes) and scale / offset dwords.
+// (u32x8) or int8 (u8, s8) codes, with the loads and the arithmetic in
+// different waves. A workgroup owns NR = 16 NB weight rows and all of K,
+// cut into items of four groups (K = 256): x (16 rows x 512 bytes), codes
+// (NR rows x 128 bytes for int4, 256 for int8) and scale / offset dwords.
 //  - Two producer waves move items (the even and the odd ones) from
 //    global memory into a ring of S slots in LDS by LDS DMA, each with up
-//    to three items in flight (the most the memory counter of one wave,
-//    63 instructions, can tell apart). A producer never computes, so the
+//    to kFly items in flight (three for int4, two for int8: the most the
+//    memory counter of one wave, 63 instructions, can tell apart). A producer never computes, so the
 //    memory queue stays full.
 //  - NC consumer waves (consumer c takes items c, c + NC, ...) read the
 //    items from LDS and compute. A consumer never issues a global load,
@@ -393,31 +393,35 @@ auto Skinny8() {
 // The arithmetic is that of qmm_skinny_kernel with MB = 1; the consumers'
 // partial tiles are summed through LDS at the end. Measured against the
 // register-staged kernel at M = 16: 12288 x 4096 11.8 vs 12.5 us, 4096 x
-// 12288 13.6 vs 14.7 us; it is used when every workgroup fits on the GPU
-// at once (the lm_head's 3166 row blocks run faster on the register-staged
+// 12288 13.6 vs 14.7 us (int8 at M = 8, 12288 x 4096: 14.8 vs 16.5 us);
+// it is used when every workgroup fits on the GPU at once (the lm_head's 3166 row blocks run faster on the register-staged
 // kernel, whose workgroups overlap one another).
-template <int NB>
+template <int PACK, int NB>
 constexpr int WsSlotBytes() {
   // x, codes (whole 1 KB DMA instructions), scales and offsets (two dwords
   // per row, whole 256-byte instructions)
-  return 8192 + ((128 * 16 * NB + 1023) / 1024) * 1024 +
+  return 8192 +
+         (((PACK == QK_PACK_U32X8 ? 128 : 256) * 16 * NB + 1023) / 1024) *
+             1024 +
          2 * ((32 * NB + 63) / 64) * 256;
 }
 constexpr int kWsConsumers = 8, kWsProducers = 2;
 
-template <int NB>
+template <int PACK, int NB>
 __global__ __launch_bounds__((kWsConsumers + kWsProducers) * 64) void
 qmm_ws_kernel(SkArgs a) {
+  constexpr bool kInt4 = PACK == QK_PACK_U32X8;
+  constexpr int CB = kInt4 ? 128 : 256;        // code bytes per row and item
   constexpr int NC = kWsConsumers, NP = kWsProducers;
   constexpr int NR = 16 * NB;                  // weight rows per workgroup
   constexpr int TS = NR + 1;                   // partial-tile row stride
-  constexpr int kCDma = (NR * 128 + 1023) / 1024;
+  constexpr int kCDma = (NR * CB + 1023) / 1024;
   constexpr int kSDma = (NR * 2 + 63) / 64;
   constexpr int kCOff = 8192, kSOff = kCOff + kCDma * 1024,
                 kBOff = kSOff + kSDma * 256;
-  constexpr int kSlot = WsSlotBytes<NB>();
+  constexpr int kSlot = WsSlotBytes<PACK, NB>();
   constexpr int kDma = 8 + kCDma + 2 * kSDma;  // DMA instructions per item
-  constexpr int kFly = 3;                      // items in flight / producer
+  constexpr int kFly = 63 / kDma < 3 ? 63 / kDma : 3;  // in flight / producer
   constexpr int S = (150 * 1024) / kSlot;      // ring slots
   static_assert(kBOff + kSDma * 256 == kSlot, "slot layout");
   static_assert(kFly * kDma <= 63, "memory counter");
@@ -456,11 +460,14 @@ qmm_ws_kernel(SkArgs a) {
     // of a row is stored in place j ^ sw(row), so that the rows of one
     // fragment read fall in distinct banks:
     //  x: 2 rows of 512 bytes per instruction, sw(r) = r & 7;
-    //  codes: 8 rows of 128 bytes per instruction, sw(r) = (r / 2) & 7;
+    //  int4 codes: 8 rows of 128 bytes per instruction, sw(r) = (r / 2) & 7
+    //    (the 16 rows of an 8-byte read fall in 16 distinct places);
+    //  int8 codes: 4 rows of 256 bytes per instruction, sw(r) = r & 7 (the
+    //    8 rows of a 16-byte read pass);
     //  scales / offsets: lane L, row n0 + L / 2, dword L % 2 (groups
     //    4 j + 2 (L % 2) and 4 j + 2 (L % 2) + 1).
     const int p = wave - NC;
-    const int row_bytes = a.k / 2;
+    const int row_bytes = kInt4 ? a.k / 2 : a.k;
     DmaRsrc crs, xrs, srs, brs;
     crs.make(a.codes, static_cast<long long>(a.n) * row_bytes);
     xrs.make(a.x, static_cast<long long>(a.m) * a.k * 2);
@@ -475,11 +482,11 @@ qmm_ws_kernel(SkArgs a) {
     int cvo[kCDma];
 #pragma unroll
     for (int i = 0; i < kCDma; ++i) {
-      const int rr = 8 * i + lane / 8, q = lane % 8;
+      constexpr int LPR = CB / 16;  // lanes per code row
+      const int rr = (64 / LPR) * i + lane / LPR, q = lane % LPR;
       const int r = n0 + rr;
-      cvo[i] = (rr < NR && r < a.n)
-                   ? r * row_bytes + ((q ^ ((rr >> 1) & 7)) << 4)
-                   : kOut;
+      const int sw = kInt4 ? (rr >> 1) & 7 : rr & 7;
+      cvo[i] = (rr < NR && r < a.n) ? r * row_bytes + ((q ^ sw) << 4) : kOut;
     }
     int svo[kSDma];
 #pragma unroll
@@ -507,7 +514,7 @@ qmm_ws_kernel(SkArgs a) {
       const int g = 4 * j;
 #pragma unroll
       for (int i = 0; i < kCDma; ++i)
-        crs.dma_nt(slot + kCOff + i * 1024, cvo[i], g * 32);
+        crs.dma_nt(slot + kCOff + i * 1024, cvo[i], g * (CB / 4));
 #pragma unroll
       for (int i = 0; i < kSDma; ++i) {
         srs.dma4(slot + kSOff + i * 256, svo[i], g * 2);
@@ -542,8 +549,9 @@ qmm_ws_kernel(SkArgs a) {
       // x chunks 2 (l / 16) and 2 (l / 16) + 1 of row l % 16, its code
       // words 2 (l / 16) and 2 (l / 16) + 1 of each row block, and the
       // group's scale and offset of each row block.
+      using CodeT = typename std::conditional<kInt4, u32x2, u32x4>::type;
       u32x4 xv[4][2];
-      u32x2 wv[4][NB];
+      CodeT wv[4][NB];
       uint32_t sv[2][NB], bv[2][NB];
 #pragma unroll
       for (int gg = 0; gg < 4; ++gg) {
@@ -555,10 +563,19 @@ qmm_ws_kernel(SkArgs a) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
           const int r = 16 * nb + l16;
-          const int c = 2 * gg + (q16 >> 1);
-          wv[gg][nb] = *reinterpret_cast<const u32x2*>(
-              slot + kCOff + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) +
-              ((q16 & 1) << 3));
+          if constexpr (kInt4) {
+            // code words 2 (l / 16), + 1 of the group: 8 bytes of chunk
+            // 2 gg + (l / 16) / 2
+            const int c = 2 * gg + (q16 >> 1);
+            wv[gg][nb] = *reinterpret_cast<const u32x2*>(
+                slot + kCOff + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) +
+                ((q16 & 1) << 3));
+          } else {
+            // codes 16 (l / 16) .. + 15 of the group: chunk 4 gg + l / 16
+            const int c = 4 * gg + q16;
+            wv[gg][nb] = *reinterpret_cast<const u32x4*>(
+                slot + kCOff + r * 256 + ((c ^ (r & 7)) << 4));
+          }
         }
       }
 #pragma unroll
@@ -576,21 +593,32 @@ qmm_ws_kernel(SkArgs a) {
       if (lane == 0) LdsStoreVolatile(freed + s, j + 1);
 #pragma unroll
       for (int gg = 0; gg < 4; ++gg) {
-        const bf16x8 x0 = XPairs(xv[gg][0]), x1 = XPairs(xv[gg][1]);
+        // int4: x in the pair order of the code words; int8: as loaded
+        const bf16x8 x0 = kInt4 ? XPairs(xv[gg][0])
+                                : __builtin_bit_cast(bf16x8, xv[gg][0]);
+        const bf16x8 x1 = kInt4 ? XPairs(xv[gg][1])
+                                : __builtin_bit_cast(bf16x8, xv[gg][1]);
         f32x4 xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
             x0, ones, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, ones, xs, 0, 0, 0);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
+          bf16x8 b0, b1;
+          if constexpr (kInt4) {
+            b0 = CodePairs(wv[gg][nb][0], kMask, kBias);
+            b1 = CodePairs(wv[gg][nb][1], kMask, kBias);
+          } else {
+            b0 = CodeBytes<PACK>(wv[gg][nb][0], wv[gg][nb][1]);
+            b1 = CodeBytes<PACK>(wv[gg][nb][2], wv[gg][nb][3]);
+          }
           f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              x0, CodePairs(wv[gg][nb][0], kMask, kBias),
-              f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-          tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              x1, CodePairs(wv[gg][nb][1], kMask, kBias), tmp, 0, 0, 0);
+              x0, b0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, b1, tmp, 0, 0, 0);
           const int sh = 16 * (gg & 1);
           const float sc = __uint_as_float((sv[gg >> 1][nb] >> sh) << 16);
           const float of = __uint_as_float((bv[gg >> 1][nb] >> sh) << 16);
-          const float off = of - 128.f * sc;  // codes enter as q + 128
+          // int4 and signed int8 codes enter as q + 128
+          const float off = PACK == QK_PACK_U8 ? of : of - 128.f * sc;
 #pragma unroll
           for (int r = 0; r < 4; ++r)
             acc[nb][r] = fmaf(sc, tmp[r], fmaf(off, xs[r], acc[nb][r]));
@@ -674,15 +702,26 @@ qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream) {
                     : (a.n + 31) / 32 <= cus ? 2
                     : (a.n + 47) / 48 <= cus ? 3
                                              : 0;
-  if (int4 && mb == 1 && !ws_off && a.groups % 4 == 0 && ws_nb > 0) {
+  if (mb == 1 && !ws_off && a.groups % 4 == 0 && ws_nb > 0) {
     const int grid = (a.n + 16 * ws_nb - 1) / (16 * ws_nb);
     constexpr int threads = (kWsConsumers + kWsProducers) * 64;
-    if (ws_nb == 3)
-      qmm_ws_kernel<3><<<grid, threads, 0, stream>>>(a);
-    else if (ws_nb == 2)
-      qmm_ws_kernel<2><<<grid, threads, 0, stream>>>(a);
+    auto go = [&](auto k1, auto k2, auto k3) {
+      if (ws_nb == 3)
+        k3<<<grid, threads, 0, stream>>>(a);
+      else if (ws_nb == 2)
+        k2<<<grid, threads, 0, stream>>>(a);
+      else
+        k1<<<grid, threads, 0, stream>>>(a);
+    };
+#define QK_WS(P) \
+  go(qmm_ws_kernel<P, 1>, qmm_ws_kernel<P, 2>, qmm_ws_kernel<P, 3>)
+    if (p.packing == QK_PACK_U32X8)
+      QK_WS(QK_PACK_U32X8);
+    else if (p.packing == QK_PACK_U8)
+      QK_WS(QK_PACK_U8);
     else
-      qmm_ws_kernel<1><<<grid, threads, 0, stream>>>(a);
+      QK_WS(QK_PACK_S8_SYM);
+#undef QK_WS
     return PostLaunch("qmm_ws");
   }
   const int cg = int4 && mb <= 2 ? 4 : 2;
