@@ -373,11 +373,13 @@ auto Skinny8() {
     return static_cast<K>(nullptr);
 }
 
-// The streamed form for one block of 16 rows of x (M <= 16) and int4
+// The streamed form for one or two blocks of 16 rows of x and int4
 // (u32x8) or int8 (u8, s8) codes, with the loads and the arithmetic in
 // different waves. A workgroup owns NR = 16 NB weight rows and all of K,
-// cut into items of four groups (K = 256): x (16 rows x 512 bytes), codes
-// (NR rows x 128 bytes for int4, 256 for int8) and scale / offset dwords.
+// cut into items of four groups (K = 256): x (16 MB rows x 512 bytes),
+// codes (NR rows x 128 bytes for int4, 256 for int8) and scale / offset
+// dwords. int8 takes MB = 1 only (two row blocks of x would not fit the
+// registers at 48 weight rows).
 //  - Two producer waves move items (the even and the odd ones) from
 //    global memory into a ring of S slots in LDS by LDS DMA, each with up
 //    to kFly items in flight (three for int4, two for int8: the most the
@@ -394,20 +396,22 @@ auto Skinny8() {
 // partial tiles are summed through LDS at the end. Measured against the
 // register-staged kernel at M = 16: 12288 x 4096 11.8 vs 12.5 us, 4096 x
 // 12288 13.6 vs 14.7 us (int8 at M = 8, 12288 x 4096: 14.8 vs 16.5 us);
-// it is used when every workgroup fits on the GPU at once (the lm_head's 3166 row blocks run faster on the register-staged
-// kernel, whose workgroups overlap one another).
-template <int PACK, int NB>
+// it is used when every workgroup fits on the GPU at once (the lm_head's
+// 3166 row blocks run faster on the register-staged kernel, whose
+// workgroups overlap one another). MB = 2 takes 17..32 rows of x (x of an
+// item 32 rows x 512 bytes).
+template <int PACK, int MB, int NB>
 constexpr int WsSlotBytes() {
   // x, codes (whole 1 KB DMA instructions), scales and offsets (two dwords
   // per row, whole 256-byte instructions)
-  return 8192 +
+  return 8192 * MB +
          (((PACK == QK_PACK_U32X8 ? 128 : 256) * 16 * NB + 1023) / 1024) *
              1024 +
          2 * ((32 * NB + 63) / 64) * 256;
 }
 constexpr int kWsConsumers = 8, kWsProducers = 2;
 
-template <int PACK, int NB>
+template <int PACK, int MB, int NB>
 __global__ __launch_bounds__((kWsConsumers + kWsProducers) * 64) void
 qmm_ws_kernel(SkArgs a) {
   constexpr bool kInt4 = PACK == QK_PACK_U32X8;
@@ -415,18 +419,19 @@ qmm_ws_kernel(SkArgs a) {
   constexpr int NC = kWsConsumers, NP = kWsProducers;
   constexpr int NR = 16 * NB;                  // weight rows per workgroup
   constexpr int TS = NR + 1;                   // partial-tile row stride
+  constexpr int TM = 16 * MB;                  // rows of x
   constexpr int kCDma = (NR * CB + 1023) / 1024;
   constexpr int kSDma = (NR * 2 + 63) / 64;
-  constexpr int kCOff = 8192, kSOff = kCOff + kCDma * 1024,
+  constexpr int kCOff = 8192 * MB, kSOff = kCOff + kCDma * 1024,
                 kBOff = kSOff + kSDma * 256;
-  constexpr int kSlot = WsSlotBytes<PACK, NB>();
-  constexpr int kDma = 8 + kCDma + 2 * kSDma;  // DMA instructions per item
+  constexpr int kSlot = WsSlotBytes<PACK, MB, NB>();
+  constexpr int kDma = 8 * MB + kCDma + 2 * kSDma;  // DMA per item
   constexpr int kFly = 63 / kDma < 3 ? 63 / kDma : 3;  // in flight / producer
   constexpr int S = (150 * 1024) / kSlot;      // ring slots
   static_assert(kBOff + kSDma * 256 == kSlot, "slot layout");
   static_assert(kFly * kDma <= 63, "memory counter");
   static_assert(S >= NP * kFly + 1, "ring depth");
-  static_assert(S * kSlot >= NC * 16 * TS * 4, "partial tiles fit");
+  static_assert(S * kSlot >= NC * TM * TS * 4, "partial tiles fit");
   __shared__ __attribute__((aligned(16))) unsigned char ring[S * kSlot];
   __shared__ uint32_t flags[2 * S];  // ready[S], freed[S]
 
@@ -449,9 +454,11 @@ qmm_ws_kernel(SkArgs a) {
     }
   };
 
-  f32x4 acc[NB];
+  f32x4 acc[MB][NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (wave >= NC) {
     // Producer p = wave - NC moves items p, p + NP, ... Lane maps (each
@@ -473,9 +480,9 @@ qmm_ws_kernel(SkArgs a) {
     xrs.make(a.x, static_cast<long long>(a.m) * a.k * 2);
     srs.make(a.scales, static_cast<long long>(a.n) * G * 2);
     brs.make(a.biases, a.has_bias ? static_cast<long long>(a.n) * G * 2 : 0);
-    int xvo[8];
+    int xvo[8 * MB];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 8 * MB; ++i) {
       const int r = 2 * i + lane / 32, q = lane % 32;
       xvo[i] = (r * a.k + ((q & ~7) | ((q & 7) ^ (r & 7))) * 8) * 2;
     }
@@ -521,7 +528,8 @@ qmm_ws_kernel(SkArgs a) {
         brs.dma4(slot + kBOff + i * 256, svo[i], g * 2);
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xrs.dma(slot + i * 1024, xvo[i], g * 128);
+      for (int i = 0; i < 8 * MB; ++i)
+        xrs.dma(slot + i * 1024, xvo[i], g * 128);
       ++issued;
       if (issued - published >= kFly) {
         // the oldest own item in flight has landed once at most kFly - 1
@@ -550,16 +558,18 @@ qmm_ws_kernel(SkArgs a) {
       // words 2 (l / 16) and 2 (l / 16) + 1 of each row block, and the
       // group's scale and offset of each row block.
       using CodeT = typename std::conditional<kInt4, u32x2, u32x4>::type;
-      u32x4 xv[4][2];
+      u32x4 xv[4][MB][2];
       CodeT wv[4][NB];
       uint32_t sv[2][NB], bv[2][NB];
 #pragma unroll
       for (int gg = 0; gg < 4; ++gg) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-          xv[gg][h] = *reinterpret_cast<const u32x4*>(
-              slot + l16 * 512 +
-              ((8 * gg + ((2 * q16 + h) ^ (l16 & 7))) << 4));
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            xv[gg][mb][h] = *reinterpret_cast<const u32x4*>(
+                slot + (16 * mb + l16) * 512 +
+                ((8 * gg + ((2 * q16 + h) ^ (l16 & 7))) << 4));
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
           const int r = 16 * nb + l16;
@@ -594,13 +604,19 @@ qmm_ws_kernel(SkArgs a) {
 #pragma unroll
       for (int gg = 0; gg < 4; ++gg) {
         // int4: x in the pair order of the code words; int8: as loaded
-        const bf16x8 x0 = kInt4 ? XPairs(xv[gg][0])
-                                : __builtin_bit_cast(bf16x8, xv[gg][0]);
-        const bf16x8 x1 = kInt4 ? XPairs(xv[gg][1])
-                                : __builtin_bit_cast(bf16x8, xv[gg][1]);
-        f32x4 xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            x0, ones, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, ones, xs, 0, 0, 0);
+        bf16x8 x0[MB], x1[MB];
+        f32x4 xs[MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          x0[mb] = kInt4 ? XPairs(xv[gg][mb][0])
+                         : __builtin_bit_cast(bf16x8, xv[gg][mb][0]);
+          x1[mb] = kInt4 ? XPairs(xv[gg][mb][1])
+                         : __builtin_bit_cast(bf16x8, xv[gg][mb][1]);
+          xs[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              x0[mb], ones, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          xs[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1[mb], ones,
+                                                           xs[mb], 0, 0, 0);
+        }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
           bf16x8 b0, b1;
@@ -611,17 +627,22 @@ qmm_ws_kernel(SkArgs a) {
             b0 = CodeBytes<PACK>(wv[gg][nb][0], wv[gg][nb][1]);
             b1 = CodeBytes<PACK>(wv[gg][nb][2], wv[gg][nb][3]);
           }
-          f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              x0, b0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-          tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, b1, tmp, 0, 0, 0);
           const int sh = 16 * (gg & 1);
           const float sc = __uint_as_float((sv[gg >> 1][nb] >> sh) << 16);
           const float of = __uint_as_float((bv[gg >> 1][nb] >> sh) << 16);
           // int4 and signed int8 codes enter as q + 128
           const float off = PACK == QK_PACK_U8 ? of : of - 128.f * sc;
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            acc[nb][r] = fmaf(sc, tmp[r], fmaf(off, xs[r], acc[nb][r]));
+          for (int mb = 0; mb < MB; ++mb) {
+            f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                x0[mb], b0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1[mb], b1, tmp, 0,
+                                                          0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[mb][nb][r] =
+                  fmaf(sc, tmp[r], fmaf(off, xs[mb][r], acc[mb][nb][r]));
+          }
         }
       }
     }
@@ -634,19 +655,22 @@ qmm_ws_kernel(SkArgs a) {
   if (wave < NC) {
     const int q16 = lane >> 4, l16 = lane & 15;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        part[(wave * 16 + 4 * q16 + r) * TS + 16 * nb + l16] = acc[nb][r];
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          part[(wave * TM + 16 * mb + 4 * q16 + r) * TS + 16 * nb + l16] =
+              acc[mb][nb][r];
   }
   __syncthreads();
   bf16* Y = static_cast<bf16*>(a.y);
-  for (int e = threadIdx.x; e < 16 * NR; e += (NC + NP) * 64) {
+  for (int e = threadIdx.x; e < TM * NR; e += (NC + NP) * 64) {
     const int r = e / NR, c = e % NR;
     if (r >= a.m || n0 + c >= a.n) continue;
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < NC; ++w) v += part[(w * 16 + r) * TS + c];
+    for (int w = 0; w < NC; ++w) v += part[(w * TM + r) * TS + c];
     Y[static_cast<long long>(r) * a.n + n0 + c] = from_f32<bf16>(v);
   }
 }
@@ -702,7 +726,8 @@ qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream) {
                     : (a.n + 31) / 32 <= cus ? 2
                     : (a.n + 47) / 48 <= cus ? 3
                                              : 0;
-  if (mb == 1 && !ws_off && a.groups % 4 == 0 && ws_nb > 0) {
+  // int8 with two row blocks of x would not fit the registers at 48 rows.
+  if (mb <= (int4 ? 2 : 1) && !ws_off && a.groups % 4 == 0 && ws_nb > 0) {
     const int grid = (a.n + 16 * ws_nb - 1) / (16 * ws_nb);
     constexpr int threads = (kWsConsumers + kWsProducers) * 64;
     auto go = [&](auto k1, auto k2, auto k3) {
@@ -713,14 +738,16 @@ qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream) {
       else
         k1<<<grid, threads, 0, stream>>>(a);
     };
-#define QK_WS(P) \
-  go(qmm_ws_kernel<P, 1>, qmm_ws_kernel<P, 2>, qmm_ws_kernel<P, 3>)
-    if (p.packing == QK_PACK_U32X8)
-      QK_WS(QK_PACK_U32X8);
-    else if (p.packing == QK_PACK_U8)
-      QK_WS(QK_PACK_U8);
-    else
-      QK_WS(QK_PACK_S8_SYM);
+#define QK_WS(P, MB) \
+  go(qmm_ws_kernel<P, MB, 1>, qmm_ws_kernel<P, MB, 2>, \
+     qmm_ws_kernel<P, MB, 3>)
+    if (p.packing == QK_PACK_U32X8) {
+      if (mb == 1) QK_WS(QK_PACK_U32X8, 1); else QK_WS(QK_PACK_U32X8, 2);
+    } else if (p.packing == QK_PACK_U8) {
+      QK_WS(QK_PACK_U8, 1);
+    } else {
+      QK_WS(QK_PACK_S8_SYM, 1);
+    }
 #undef QK_WS
     return PostLaunch("qmm_ws");
   }

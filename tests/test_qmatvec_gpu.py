@@ -121,7 +121,7 @@ def test_qmatvec_single_row_paths(dev, packing, k):
 @pytest.mark.parametrize("mnk", [(5, 300, 4096), (8, 77, 1024),
                                  (16, 4096, 4096), (16, 6000, 1024),
                                  (12, 9000, 3072), (16, 12400, 1024),
-                                 (32, 1000, 512),
+                                 (32, 1000, 512), (27, 9000, 2048),
                                  (33, 64, 1024), (40, 520, 12288),
                                  (64, 2048, 2048)])
 @pytest.mark.parametrize("packing", [Packing.U32X8, Packing.U8,
@@ -134,7 +134,9 @@ def test_qmatvec_few_rows(dev, mnk, packing):
     16 rows: the streamed kernel with 16, 32 and 48 weight rows per
     workgroup (N = 4096, 6000, 9000; the last two with a partly filled
     workgroup) and the register-staged one with 48 (N = 12400, more
-    workgroups than CUs), K of 4, 12 and 64 items of four groups."""
+    workgroups than CUs), K of 4, 12 and 64 items of four groups; for
+    int4 and 17..32 rows the streamed kernel with two row blocks of x
+    (M = 32, 27)."""
     m, n, k = mnk
     rng = np.random.default_rng(m * 7 + n)
     for has_bias in (True, False):
