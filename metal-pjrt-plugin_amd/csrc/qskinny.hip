@@ -1,5 +1,5 @@
-// Quantized matmul for a few rows of x (5 <= M <= 64 as routed; the kernel
-// takes 1..64): y[M, N] = x[M, K] W^T with W int4 (u32x8 words), bf16 x /
+// Quantized matmul for a few rows of x (5 <= M <= 32 as routed; the kernels
+// take 1..32): y[M, N] = x[M, K] W^T with W int4 (u32x8 words), bf16 x /
 // scale / offset, group size 64: the batched-decode and short-prefill
 // shapes. The reference's linear() (examples/llm/qwen3.py:215-230)
 // dequantizes W to x's type for more than ROWS_MAX = 4 rows and multiplies;
@@ -683,7 +683,9 @@ bool QSkinnyApplies(const QuantProblem& p) {
   const bool int8 = p.bits == 8 && (p.packing == QK_PACK_U8 ||
                                     p.packing == QK_PACK_S8_SYM);
   const int64_t row_bytes = int4 ? p.k / 2 : p.k;
-  return m >= 1 && m <= (int4 ? 64 : 32) && (int4 || int8) && p.group == 64 &&
+  // Above 32 rows the dequantizing qmm_mid_kernel is faster (int4 at
+  // 12288 x 4096: M = 33 25.5 vs 29.9 us, M = 64 28.4 vs 38.0 us).
+  return m >= 1 && m <= 32 && (int4 || int8) && p.group == 64 &&
          p.x_dtype == QK_BF16 && p.scale_dtype == QK_BF16 &&
          (!p.has_bias || p.bias_dtype == QK_BF16) && p.k % 1024 == 0 &&
          p.k > 0 && p.n > 0 && p.n * row_bytes < (int64_t{1} << 31) &&
@@ -709,10 +711,10 @@ qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream) {
   a.has_bias = p.has_bias ? 1 : 0;
   const int cus = DeviceComputeUnits();
   const int mb = (a.m + 15) / 16;
-  // Sub-chunks of 4 groups (2 for more than 32 rows of x, to bound the
+  // Register-staged kernel: sub-chunks of 4 groups (int8: 2, to bound the
   // registers); 32 weight rows per workgroup when that still gives every
-  // CU one (16 for more than 32 rows of x); eight waves split K (fewer
-  // when K is short), each walking k / KW.
+  // CU one; eight waves split K (fewer when K is short), each walking
+  // k / KW.
   const bool int4 = p.packing == QK_PACK_U32X8;
   // QK_SKINNY_WS=0 turns the streamed kernel off (tuning).
   static const bool ws_off = [] {
@@ -799,15 +801,9 @@ qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream) {
         else if (wide) QK_SKINNY(QK_PACK_U32X8, 1, 2, 4);
         else QK_SKINNY(QK_PACK_U32X8, 1, 1, 4);
         break;
-      case 2:
+      default:  // 17..32 rows
         if (wide) QK_SKINNY(QK_PACK_U32X8, 2, 2, 4);
         else QK_SKINNY(QK_PACK_U32X8, 2, 1, 4);
-        break;
-      case 3:
-        QK_SKINNY(QK_PACK_U32X8, 3, 1, 2);
-        break;
-      default:
-        QK_SKINNY(QK_PACK_U32X8, 4, 1, 2);
         break;
     }
   } else if (p.packing == QK_PACK_U8) {

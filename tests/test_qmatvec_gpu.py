@@ -128,7 +128,7 @@ def test_qmatvec_single_row_paths(dev, packing, k):
                                      Packing.S8_SYM])
 def test_qmatvec_few_rows(dev, mnk, packing):
     """5..64 rows of bf16 x with group-64 int4 u32x8 or int8 codes (the
-    streaming MFMA kernels up to 64 / 32 rows, the dequantizing paths
+    streaming MFMA kernels up to 32 rows, the dequantizing paths
     beyond): ragged N, one to four 16-row blocks, long K, with and without
     offsets, elementwise against the float64 oracle. For int4 and at most
     16 rows: the streamed kernel with 16, 32 and 48 weight rows per
