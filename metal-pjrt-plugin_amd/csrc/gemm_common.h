@@ -596,9 +596,10 @@ __device__ __forceinline__ void store_direct(
   else go(T{});
 }
 
-template <typename T, int BN, bool TA, class BSrc>
-__global__ __launch_bounds__(256) void gemm_fast_kernel(GemmArgs g) {
-  constexpr int BM = 256, BK = 64, NT = 256, WM = 2, WN = 2;
+template <typename T, int BN, bool TA, class BSrc, int NW = 4, int BM = 256>
+__global__ __launch_bounds__(NW * 64) void gemm_fast_kernel(GemmArgs g) {
+  constexpr int BK = 64, NT = NW * 64, WM = NW / 2, WN = 2;
+  static_assert(BSrc::NT == NT, "B loader built for this workgroup");
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
   constexpr bool AK = !TA, BKC = BSrc::kKCont;  // K-contiguous operands
   using LA = TileLayout<T, BM, BK, AK>;

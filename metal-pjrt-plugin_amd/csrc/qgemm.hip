@@ -15,6 +15,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 #include <string>
 
 #include "gemm_common.h"
@@ -163,22 +164,24 @@ struct QuantB {
 };
 
 // Quantized B operand of the interior-tile kernel (gemm_common.h): weight
-// rows n0 .. n0 + BN of a K tile of 64 = one group of 64. Each thread
-// buffer-loads its part of one row's codes (16-byte loads, every row's
-// bytes contiguous across its TPR threads) and the group's bf16 scale and
-// offset, and writes T(f32(q) * f32(s) + f32(b)) (the unfused canonical
-// rounding of qk$dequantize) K-contiguously into LDS.
-template <int PACK, typename T, int BN>
+// rows n0 .. n0 + BN of a K tile of 64 = one group of 64. Each of the NT
+// threads buffer-loads its part of one row's codes (16-byte loads, or one
+// 8-byte load for 16 int4 codes; every row's bytes contiguous across its
+// TPR threads) and the group's bf16 scale and offset, and writes
+// T(f32(q) * f32(s) + f32(b)) (the unfused canonical rounding of
+// qk$dequantize) K-contiguously into LDS.
+template <int PACK, typename T, int BN, int NT_ = 256>
 struct QuantFastB {
   static constexpr bool kKCont = true;
   static constexpr bool kInt4 = PACK == QK_PACK_U32X8;
-  static constexpr int NT = 256, BK = 64;
+  static constexpr int NT = NT_, BK = 64;
   static constexpr int TPR = NT / BN;                // threads per row
   static constexpr int KPT = BK / TPR;               // codes per thread
-  static constexpr int NL = (kInt4 ? KPT / 2 : KPT) / 16;  // 16 B loads
+  static constexpr int CBT = kInt4 ? KPT / 2 : KPT;  // code bytes per thread
+  static constexpr int NL = CBT >= 16 ? CBT / 16 : 1;  // loads
   static constexpr int NV = KPT * static_cast<int>(sizeof(T)) / 16;
   static constexpr int LD = TileLayout<T, BN, BK, true>::kLd;
-  static_assert(NL >= 1 && NV >= 1, "tile split");
+  static_assert((CBT == 8 || CBT % 16 == 0) && NV >= 1, "tile split");
   __amdgpu_buffer_rsrc_t crs, srs, brs;
   int row_bytes, G, r, kk0, cvo, svo;
   u32x4 c[NL];
@@ -200,9 +203,14 @@ struct QuantFastB {
   }
   __device__ __forceinline__ void load(int n0, int k0) {
     const int so = n0 * row_bytes + (kInt4 ? k0 / 2 : k0);
+    if constexpr (CBT == 8) {
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(crs, cvo, so, 2);
+      c[0] = u32x4{v[0], v[1], 0u, 0u};
+    } else {
 #pragma unroll
-    for (int i = 0; i < NL; ++i)
-      c[i] = __builtin_amdgcn_raw_buffer_load_b128(crs, cvo + 16 * i, so, 2);
+      for (int i = 0; i < NL; ++i)
+        c[i] = __builtin_amdgcn_raw_buffer_load_b128(crs, cvo + 16 * i, so, 2);
+    }
     const int sg = n0 * G * 2 + (k0 / 64) * 2;
     sraw = __builtin_amdgcn_raw_buffer_load_b16(srs, svo, sg, 0);
     braw = __builtin_amdgcn_raw_buffer_load_b16(brs, svo, sg, 0);  // 0: none
@@ -237,15 +245,17 @@ struct QuantFastB {
   }
 };
 
-// The interior-tile kernel for M a multiple of 256, N of 128, group 64,
-// bf16 scales/offsets; false when it does not apply.
+// The interior-tile kernel for M a multiple of 128, N of 128, group 64,
+// bf16 scales/offsets; false when it does not apply. Eight waves; tiles
+// of 256 x 256, 256 x 128 or 128 x 128 (two workgroups per CU), the
+// largest that leaves no CU idle.
 template <typename T, int PACK>
 bool LaunchFastQ(GemmArgs g, int m, int n, hipStream_t stream,
                  qk_status* st) {
   if constexpr (PACK == QK_PACK_BYTE_HALFSPLIT) {
     return false;
   } else {
-    if (m % 256 != 0 || n % 128 != 0 || g.k % 64 != 0 || g.k == 0 ||
+    if (m % 128 != 0 || n % 128 != 0 || g.k % 64 != 0 || g.k == 0 ||
         g.qgroup != 64 || g.qsdt != QK_BF16 ||
         (g.qhas_bias && g.qbdt != QK_BF16) ||
         static_cast<int64_t>(n) * g.qrow_bytes >= (int64_t{1} << 31) ||
@@ -254,16 +264,46 @@ bool LaunchFastQ(GemmArgs g, int m, int n, hipStream_t stream,
         reinterpret_cast<uintptr_t>(g.b) % 16 != 0)
       return false;
     const int cus = DeviceComputeUnits();
-    const bool wide = n % 256 == 0 && (m / 256) * (n / 256) >= cus;
-    g.tiles_m = m / 256;
-    g.tiles_n = n / (wide ? 256 : 128);
+    // QK_QGEMM_TILE=1|2|3 forces 256x256 / 256x128 / 128x128 (tuning).
+    static const int forced = [] {
+      const char* v = std::getenv("QK_QGEMM_TILE");
+      return v == nullptr ? 0 : std::atoi(v);
+    }();
+    // Tile choice, measured at N = 12288, K = 4096 (int4, us): M = 256:
+    // 114 / 75 / 63; M = 512: 130 / 82 / 112; M = 1024: 139 / 162 / 187;
+    // M = 2048: 271 / 259 / 382 (256x256 / 256x128 / 128x128). The
+    // smallest tile whose count still fits one round of CUs; when none
+    // does, the fewest rounds times tile size (ties to the larger tile).
+    const bool ok[4] = {false, m % 256 == 0 && n % 256 == 0, m % 256 == 0,
+                        true};
+    const long long count[4] = {0, (m / 256LL) * (n / 256),
+                                (m / 256LL) * (n / 128), (m / 128LL) * (n / 128)};
+    const double size[4] = {0, 1.0, 0.5, 0.25};
+    int tile = 0;
+    for (int t = 1; t <= 3; ++t)
+      if (ok[t] && count[t] <= cus) tile = t;
+    if (tile == 0) {
+      double best = 1e30;
+      for (int t = 1; t <= 3; ++t) {
+        if (!ok[t]) continue;
+        const double c = static_cast<double>((count[t] + cus - 1) / cus) * size[t];
+        if (c < best) best = c, tile = t;
+      }
+    }
+    if (forced >= 1 && forced <= 3 && ok[forced]) tile = forced;
+    const int bm = tile == 3 ? 128 : 256, bn = tile == 1 ? 256 : 128;
+    g.tiles_m = m / bm;
+    g.tiles_n = n / bn;
     const dim3 grid(g.tiles_m * g.tiles_n);
-    if (wide)
-      gemm_fast_kernel<T, 256, false, QuantFastB<PACK, T, 256>>
-          <<<grid, 256, 0, stream>>>(g);
+    if (tile == 1)
+      gemm_fast_kernel<T, 256, false, QuantFastB<PACK, T, 256, 512>, 8>
+          <<<grid, 512, 0, stream>>>(g);
+    else if (tile == 2)
+      gemm_fast_kernel<T, 128, false, QuantFastB<PACK, T, 128, 512>, 8>
+          <<<grid, 512, 0, stream>>>(g);
     else
-      gemm_fast_kernel<T, 128, false, QuantFastB<PACK, T, 128>>
-          <<<grid, 256, 0, stream>>>(g);
+      gemm_fast_kernel<T, 128, false, QuantFastB<PACK, T, 128, 512>, 8, 128>
+          <<<grid, 512, 0, stream>>>(g);
     *st = PostLaunch("qgemm_fast");
     return true;
   }

@@ -185,12 +185,15 @@ def test_qmatvec_mid_rows(dev, mnk, packing):
     (512, 1024, 2048, Packing.U8, "bfloat16"),
     (256, 512, 1024, Packing.S8_SYM, "bfloat16"),
     (256, 256, 512, Packing.U32X8, "float16"),
-    (2048, 8192, 256, Packing.U32X8, "bfloat16"),  # 256-column tiles
+    (2048, 8192, 256, Packing.U32X8, "bfloat16"),  # 256 x 256 tiles
+    (512, 12288, 256, Packing.U32X8, "bfloat16"),  # 256 x 128 tiles
+    (384, 1024, 512, Packing.U8, "bfloat16"),      # 128 x 128, M % 256 != 0
 ])
 def test_qmatvec_prefill_tiles(dev, case):
-    """Row counts that are multiples of 256 (the interior-tile GEMM with
-    the dequantizing B loader), each packing it takes, bf16 and f16 x,
-    with and without offsets. Like the reference's linear() for more than
+    """Row counts that are multiples of 128 (the interior-tile GEMM with
+    the dequantizing B loader: 128 x 128, 256 x 128 and 256 x 256 tiles,
+    chosen by how many tiles one round of CUs takes), each packing it
+    takes, bf16 and f16 x, with and without offsets. Like the reference's linear() for more than
     four rows (examples/llm/qwen3.py:215-230), the weights are dequantized
     to x's type first, so the float64 oracle multiplies by those rounded
     weights."""
