@@ -712,12 +712,7 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
       for (int i = 0; i < 4; ++i) xq[i * cpr + c] = quad[i];
     }
   }
-  // Every wave waits for its first slots here. The loop below then starts
-  // from "nothing outstanding", so its waits follow the loop body's own
-  // load order; without this, merging the prologue's order makes them
-  // wait for whole rounds of prefetch.
   __syncthreads();
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   u32x4 xr[CPL][4];
   float xsum[G];
 #pragma unroll
@@ -776,11 +771,43 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
 
   bf16* Y = static_cast<bf16*>(a.y);
   int row = gw;
+  static_assert(D == 2 || D % 4 == 0, "rows are reduced four at a time");
+  constexpr int DA = D < 4 ? 4 : D;  // accumulators, padded to fours
+  // Reduce one round's partial sums and store rows row + d GW < N.
+  auto finish = [&](const float (&acc)[DA]) {
+    if (row + GW >= a.n) {  // one row this round (small matrices)
+      const float v = wave_sum_dpp(acc[0]);
+      if (lane == 0) Y[row] = from_f32<bf16>(v);
+    } else {
+      // Lane l < 4 gets the total of row row + (q + l) * GW.
+#pragma unroll
+      for (int q = 0; q < DA; q += 4) {
+        const float v = wave_sum4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3],
+                                  lane);
+        const int rr = row + (q + (lane & 3)) * GW;
+        if (lane < 4 && q + lane < D && rr < a.n) Y[rr] = from_f32<bf16>(v);
+      }
+    }
+  };
+  if (row + D * GW >= a.n) {
+    // All of this wave's rows are in its first slots (one round): each row
+    // is computed as soon as its own loads have landed (the loads complete
+    // in order), while the later rows are still in flight.
+    float acc[DA] = {};
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (row + d * GW < a.n) acc[d] = row_acc(buf[d]);
+    finish(acc);
+    return;
+  }
+  // Every wave waits for its first slots here. The loop below then starts
+  // from "nothing outstanding", so its waits follow the loop body's own
+  // load order; without this, merging the prologue's order makes them
+  // wait for whole rounds of prefetch.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   // Steady state: this round's rows and the next round's are all in
   // range, so the prefetch is unconditional (no merge of old and new
   // slot contents that would wait on the loads just issued).
-  static_assert(D == 2 || D % 4 == 0, "rows are reduced four at a time");
-  constexpr int DA = D < 4 ? 4 : D;  // accumulators, padded to fours
   for (; row + (2 * D - 1) * GW < a.n; row += D * GW) {
     float acc[DA] = {};
 #pragma unroll
@@ -806,19 +833,7 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_kernel(QmvArgs a) {
         if (nr < a.n) load_row(nr, buf[d]);
       }
     }
-    if (row + GW >= a.n) {  // one row this round (small matrices)
-      const float v = wave_sum_dpp(acc[0]);
-      if (lane == 0) Y[row] = from_f32<bf16>(v);
-    } else {
-      // Lane l < 4 gets the total of row row + (q + l) * GW.
-#pragma unroll
-      for (int q = 0; q < DA; q += 4) {
-        const float v = wave_sum4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3],
-                                  lane);
-        const int rr = row + (q + (lane & 3)) * GW;
-        if (lane < 4 && q + lane < D && rr < a.n) Y[rr] = from_f32<bf16>(v);
-      }
-    }
+    finish(acc);
   }
 }
 
