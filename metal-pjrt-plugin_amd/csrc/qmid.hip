@@ -38,6 +38,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 
 #include "qk_device.h"
 #include "qk_internal.h"
@@ -284,6 +285,206 @@ __global__ __launch_bounds__(KW * 64) void qmm_mid_kernel(MdArgs a) {
   }
 }
 
+// The producer / consumer form of qmm_mid_kernel (same slot layout, lane
+// maps and arithmetic): two producer waves move whole groups (x TM rows x
+// 128 bytes, codes NR rows x GB bytes, scale / offset dwords) from global
+// memory into a ring of S slots in LDS by LDS DMA, each with up to three
+// groups in flight; NC consumer waves (consumer c takes groups c, c + NC,
+// ...) read them from LDS, dequantize and multiply. A consumer never
+// issues a global load, so it never stalls behind a full memory queue;
+// a producer never computes, so the queue stays full. Hand-off through LDS
+// words (ready[s] = g + 1 once group g has landed in slot s = g % S,
+// freed[s] = g + 1 once its consumer has read it); every wait is a bounded
+// spin. The DMA is inline asm and the flags are read through LDS-typed
+// pointers, so the compiler adds no waits for the DMA of its own.
+constexpr int kMidConsumers = 4, kMidProducers = 2;
+
+template <int PACK, int MB, int NB>
+__global__ __launch_bounds__((kMidConsumers + kMidProducers) * 64) void
+qmm_wsmid_kernel(MdArgs a) {
+  constexpr int NC = kMidConsumers, NP = kMidProducers;
+  constexpr bool kInt4 = PACK == QK_PACK_U32X8;
+  constexpr int GB = kInt4 ? 32 : 64;  // code bytes per group per row
+  constexpr int NR = 16 * NB;          // weight rows per workgroup
+  constexpr int TM = 16 * MB, TS = NR + 1;
+  constexpr int kCRows = 1024 / GB;  // code rows per DMA instruction
+  constexpr int kCDma = (NR + kCRows - 1) / kCRows;
+  constexpr int kXOff = 0, kCOff = TM * 128, kSOff = kCOff + kCDma * 1024,
+                kBOff = kSOff + 256, kSlot = kBOff + 256;
+  constexpr int kDma = TM / 8 + kCDma + 2;  // DMA instructions per group
+  constexpr int kFly = 63 / kDma < 3 ? 63 / kDma : 3;
+  constexpr int S = (150 * 1024) / kSlot;
+  static_assert(NR <= 64, "one scale DMA per group");
+  static_assert(kFly >= 1 && S >= NP * kFly + 1, "ring depth");
+  static_assert(S * kSlot >= NC * TM * TS * 4, "partial tiles fit");
+  __shared__ __attribute__((aligned(16))) unsigned char ring[S * kSlot];
+  __shared__ uint32_t flags[2 * S];  // ready[S], freed[S]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q16 = lane >> 4, l16 = lane & 15;
+  const int n0 = blockIdx.x * NR;
+  const int G = a.groups;
+  uint32_t* const ready = flags;
+  uint32_t* const freed = flags + S;
+  if (threadIdx.x < 2 * S) LdsStoreVolatile(flags + threadIdx.x, 0);
+  __syncthreads();
+  // A spin of at most 2^20 polls (~70 ms): a wave that waits longer gives
+  // up and goes on (wrong results, but the kernel ends).
+  auto spin_until = [](const uint32_t* f, uint32_t want) {
+    for (int it = 0; it < (1 << 20); ++it) {
+      if (__builtin_amdgcn_readfirstlane(LdsLoadVolatile(f)) == want) return;
+      __builtin_amdgcn_s_sleep(1);
+    }
+  };
+
+  f32x4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (wave >= NC) {
+    // Producer p = wave - NC moves groups p, p + NP, ... (lane maps as in
+    // qmm_mid_kernel).
+    const int p = wave - NC;
+    const int row_bytes = kInt4 ? a.k / 2 : a.k;
+    DmaRsrc crs, xrs, srs, brs;
+    crs.make(a.codes, static_cast<long long>(a.n) * row_bytes);
+    xrs.make(a.x, static_cast<long long>(a.m) * a.k * 2);
+    srs.make(a.scales, static_cast<long long>(a.n) * G * 2);
+    brs.make(a.biases, a.has_bias ? static_cast<long long>(a.n) * G * 2 : 0);
+    const int xvo = ((lane >> 3) * a.k + ((lane & 7) ^ (lane >> 3)) * 8) * 2;
+    int cvo[kCDma];
+#pragma unroll
+    for (int i = 0; i < kCDma; ++i) {
+      constexpr int LPR = GB / 16;
+      const int rr = kCRows * i + lane / LPR;
+      const int sw = kInt4 ? ((rr >> 2) & 1) : ((rr >> 1) & 3);
+      const int r = n0 + rr;
+      cvo[i] = (rr < NR && r < a.n)
+                   ? r * row_bytes + (((lane % LPR) ^ sw) << 4)
+                   : kOut;
+    }
+    const int svo =
+        (lane < NR && n0 + lane < a.n) ? (n0 + lane) * G * 2 : kOut;
+    auto publish = [&](int g) {
+      if (lane == 0) LdsStoreVolatile(ready + g % S, g + 1);
+    };
+    int issued = 0, published = 0;  // own groups
+    for (int g = p; g < G; g += NP) {
+      const int s = g % S;
+      unsigned char* slot = ring + s * kSlot;
+      if (g >= S && __builtin_amdgcn_readfirstlane(LdsLoadVolatile(
+                        freed + s)) != static_cast<uint32_t>(g - S + 1)) {
+        // Publish everything in flight before waiting: a consumer of one
+        // of those groups may be what frees the slot.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        for (; published < issued; ++published) publish(p + NP * published);
+        spin_until(freed + s, g - S + 1);
+      }
+#pragma unroll
+      for (int i = 0; i < kCDma; ++i)
+        crs.dma_nt(slot + kCOff + i * 1024, cvo[i], g * GB);
+      srs.dma4(slot + kSOff, svo, (g & ~1) * 2);
+      brs.dma4(slot + kBOff, svo, (g & ~1) * 2);
+#pragma unroll
+      for (int i = 0; i < TM / 8; ++i)
+        xrs.dma(slot + kXOff + i * 1024, xvo + i * 8 * a.k * 2, g * 128);
+      ++issued;
+      if (issued - published >= kFly) {
+        // the oldest own group in flight has landed once at most kFly - 1
+        // later ones are outstanding
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kFly - 1) * kDma)
+                     : "memory");
+        publish(p + NP * published);
+        ++published;
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    for (; published < issued; ++published) publish(p + NP * published);
+  } else {
+    for (int g = wave; g < G; g += NC) {
+      const int s = g % S;
+      const unsigned char* slot = ring + s * kSlot;
+      spin_until(ready + s, g + 1);
+      asm volatile("" ::: "memory");  // the slot's reads stay below
+      const int odd = g & 1;
+      // the group's weights of each row block, dequantized (their reads
+      // complete before the slot is released)
+      bf16x8 w[NB][2];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int r = 16 * nb + l16;
+        const float sc = __uint_as_float(static_cast<uint32_t>(
+            *reinterpret_cast<const uint16_t*>(slot + kSOff + r * 4 + odd * 2))
+            << 16);
+        const float bi = __uint_as_float(static_cast<uint32_t>(
+            *reinterpret_cast<const uint16_t*>(slot + kBOff + r * 4 + odd * 2))
+            << 16);
+        if constexpr (kInt4) {
+          const int slt = (q16 >> 1) ^ ((r >> 2) & 1);
+          const u32x2 c = *reinterpret_cast<const u32x2*>(
+              slot + kCOff + r * GB + (slt << 4) + ((q16 & 1) << 3));
+          w[nb][0] = Dequant8<PACK>(c[0], 0u, sc, bi);
+          w[nb][1] = Dequant8<PACK>(c[1], 0u, sc, bi);
+        } else {
+          const int slt = q16 ^ ((r >> 1) & 3);
+          const u32x4 c = *reinterpret_cast<const u32x4*>(
+              slot + kCOff + r * GB + (slt << 4));
+          w[nb][0] = Dequant8<PACK>(c[0], c[1], sc, bi);
+          w[nb][1] = Dequant8<PACK>(c[2], c[3], sc, bi);
+        }
+      }
+      bf16x8 xv[2][MB];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const int r = 16 * mb + l16;
+          const int c = 2 * q16 + h;
+          xv[h][mb] = *reinterpret_cast<const bf16x8*>(
+              slot + kXOff + r * 128 + ((c ^ (r & 7)) << 4));
+        }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (lane == 0) LdsStoreVolatile(freed + s, g + 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                xv[h][mb], w[nb][h], acc[mb][nb], 0, 0, 0);
+    }
+  }
+
+  // Sum the consumers' partial tiles (the ring is idle: every DMA has
+  // landed and been read) and store rows < M, columns < N.
+  __syncthreads();
+  float* const part = reinterpret_cast<float*>(ring);
+  if (wave < NC) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          part[(wave * TM + 16 * mb + 4 * q16 + r) * TS + 16 * nb + l16] =
+              acc[mb][nb][r];
+  }
+  __syncthreads();
+  bf16* Y = static_cast<bf16*>(a.y);
+  for (int e = threadIdx.x; e < TM * NR; e += (NC + NP) * 64) {
+    const int r = e / NR, c = e % NR;
+    if (r >= a.m || n0 + c >= a.n) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NC; ++w) v += part[(w * TM + r) * TS + c];
+    Y[static_cast<long long>(r) * a.n + n0 + c] = from_f32<bf16>(v);
+  }
+}
+
 }  // namespace
 
 bool QMidApplies(const QuantProblem& p) {
@@ -324,9 +525,22 @@ qk_status LaunchQMid(const QuantProblem& p, hipStream_t stream) {
   const int nb = (a.n + 47) / 48 >= cus ? 3 : (a.n + 31) / 32 >= cus ? 2 : 1;
   const dim3 grid((a.n + 16 * nb - 1) / (16 * nb));
   const int mb = (a.m + 15) / 16;
+  // QK_MID_WS=0 selects the kernel whose waves load their own groups
+  // (tuning).
+  static const bool ws = [] {
+    const char* v = std::getenv("QK_MID_WS");
+    return v == nullptr || *v != '0';
+  }();
+  constexpr int kWsThreads = (kMidConsumers + kMidProducers) * 64;
 #define QK_MID_NB(P, MB)                                                  \
   do {                                                                    \
-    if (nb == 3)                                                          \
+    if (ws && nb == 3)                                                    \
+      qmm_wsmid_kernel<P, MB, 3><<<grid, kWsThreads, 0, stream>>>(a);     \
+    else if (ws && nb == 2)                                               \
+      qmm_wsmid_kernel<P, MB, 2><<<grid, kWsThreads, 0, stream>>>(a);     \
+    else if (ws)                                                          \
+      qmm_wsmid_kernel<P, MB, 1><<<grid, kWsThreads, 0, stream>>>(a);     \
+    else if (nb == 3)                                                     \
       qmm_mid_kernel<P, MB, 3, KW><<<grid, KW * 64, 0, stream>>>(a);      \
     else if (nb == 2)                                                     \
       qmm_mid_kernel<P, MB, 2, KW><<<grid, KW * 64, 0, stream>>>(a);      \
