@@ -34,6 +34,7 @@
 
 #include "gemm_common.h"
 #include "gemm_dma.h"
+#include "gemm_f32x3.h"
 #include "qk_device.h"
 #include "qk_internal.h"
 
@@ -307,6 +308,21 @@ qk_status DispatchSplitK(const GemmArgs& g, int batch, bool ta, bool tb,
   return PostLaunch(name);
 }
 
+template <int BM, int BN, int NW>
+qk_status DispatchF32x3(const GemmArgs& g, int batch, bool ta, bool tb,
+                        hipStream_t stream, const char* name) {
+  dim3 grid(g.tiles_m * g.tiles_n, batch);
+  if (!ta && !tb)
+    gemm_f32x3_kernel<BM, BN, false, false, NW><<<grid, NW * 64, 0, stream>>>(g);
+  else if (!ta && tb)
+    gemm_f32x3_kernel<BM, BN, false, true, NW><<<grid, NW * 64, 0, stream>>>(g);
+  else if (ta && !tb)
+    gemm_f32x3_kernel<BM, BN, true, false, NW><<<grid, NW * 64, 0, stream>>>(g);
+  else
+    gemm_f32x3_kernel<BM, BN, true, true, NW><<<grid, NW * 64, 0, stream>>>(g);
+  return PostLaunch(name);
+}
+
 struct TileCfg {
   int bm, bn, bk, wm, wn;
 };
@@ -355,6 +371,9 @@ constexpr HalfTile kHalfTiles[] = {
 };
 constexpr int kFastTile256 = 6, kFastTile128 = 7, kSplitK = 8, kSplitK32 = 9,
               kFastTile192 = 10;
+// f32 problems on the split-bf16 kernel (tile indices below 0: not
+// kHalfTiles entries).
+constexpr int kF32x3Tile128 = -2, kF32x3Tile64 = -3;
 constexpr int kNumHalfTiles = sizeof(kHalfTiles) / sizeof(kHalfTiles[0]);
 
 // Cost of a round of 256x192 interior tiles relative to 256x256.
@@ -369,6 +388,24 @@ int ForcedHalfTile() {
     return t >= 0 && t < kNumHalfTiles ? t : -1;
   }();
   return forced;
+}
+
+// Whether the split-bf16 f32 kernel (gemm_f32x3.h) can run the problem
+// with bm x bn tiles: f32, M, N multiples of the tile, K of 32, 16-byte
+// aligned operands and leading dimensions, and each operand of one batch
+// entry under 2^31 bytes (the extent of a buffer descriptor).
+bool F32x3Applies(const GemmProblem& p, int bm, int bn) {
+  if (p.a.dtype != QK_F32 || p.m % bm != 0 || p.n % bn != 0 ||
+      p.k % 32 != 0 || p.k == 0)
+    return false;
+  const bool batched = p.batch > 1;
+  auto ok = [&](const Operand& o, int64_t rows) {
+    const int64_t bs = batched ? o.batch_stride : 0;
+    return reinterpret_cast<uintptr_t>(o.ptr) % 16 == 0 && o.ld % 4 == 0 &&
+           bs % 4 == 0 && rows * o.ld * 4 < (int64_t{1} << 31);
+  };
+  return ok(p.a, p.a.transpose ? p.k : p.m) &&
+         ok(p.b, p.b.transpose ? p.n : p.k);
 }
 
 // Whether the interior-tile kernel can run the problem with a BN-wide
@@ -440,8 +477,22 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
     c.tile = t;
     c.bm = kHalfTiles[t].bm, c.bn = kHalfTiles[t].bn, c.bk = 64;
   } else {
+    // f32: the split-bf16 kernel on interior tiles (128x128 when those
+    // fill the GPU, else 64x64), the f32-MFMA tile kernel otherwise.
+    // QK_GEMM_F32=mfma forces the latter (tuning).
+    static const bool mfma_only = [] {
+      const char* v = std::getenv("QK_GEMM_F32");
+      return v != nullptr && std::string(v) == "mfma";
+    }();
+    const int cus = DeviceComputeUnits();
     c.tile = -1;
-    if (tiles(128, 128) >= 192) {
+    if (!mfma_only && tiles(128, 128) >= cus && F32x3Applies(p, 128, 128)) {
+      c.tile = kF32x3Tile128;
+      c.bm = 128, c.bn = 128, c.bk = 32;
+    } else if (!mfma_only && F32x3Applies(p, 64, 64)) {
+      c.tile = kF32x3Tile64;
+      c.bm = 64, c.bn = 64, c.bk = 32;
+    } else if (tiles(128, 128) >= 192) {
       c.bm = 128, c.bn = 128, c.bk = 32;
     } else {
       c.bm = 64, c.bn = 64, c.bk = 32;
@@ -450,8 +501,10 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
   const bool fast = half && (c.tile == kFastTile256 || c.tile == kFastTile192 ||
                              c.tile == kFastTile128);
   const bool splitk = c.tile == kSplitK || c.tile == kSplitK32;
+  const bool x3 = c.tile == kF32x3Tile128 || c.tile == kF32x3Tile64;
   c.name = std::string(splitk     ? (c.tile == kSplitK ? "gemm_splitk4_"
                                                        : "gemm_splitk8_")
+                       : x3       ? "gemm_f32x3_"
                        : !half    ? "gemm_mfma_"
                        : fast     ? "gemm_fast_"
                                   : "gemm_tile_") +
@@ -548,6 +601,10 @@ qk_status LaunchGemm(const GemmProblem& p, hipStream_t stream) {
     case QK_F16:
       return DispatchHalf<f16>(c.tile, g, batch, ta, tb, stream, name);
     default:
+      if (c.tile == kF32x3Tile128)
+        return DispatchF32x3<128, 128, 8>(g, batch, ta, tb, stream, name);
+      if (c.tile == kF32x3Tile64)
+        return DispatchF32x3<64, 64, 4>(g, batch, ta, tb, stream, name);
       if (c.bm == 128)
         return Dispatch<float, 128, 128, 32, 2, 2>(g, batch, ta, tb, stream, name);
       return Dispatch<float, 64, 64, 32, 2, 2>(g, batch, ta, tb, stream, name);

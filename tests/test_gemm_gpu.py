@@ -387,3 +387,50 @@ def test_config_bf16_bias_silu(dev, shape):
                                    bias.to(dev).float())
     err_all = (d.float() - ref).norm() / ref.norm()
     assert float(err_all) <= 1e-2
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_f32_split_kernel(dev, ta, tb):
+    """f32 interior tiles run on the bf16 matrix cores with each operand
+    split into three bf16 parts (gemm_f32x3.h); the product must still
+    meet the f32 tolerance: 64x64 tiles (few tiles), 128x128 tiles (a full
+    GPU of them), K of one and of several 32-wide tiles, batched with
+    padded leading dimensions, alpha / beta and an epilogue."""
+    plan = run_case(dev, 256, 192, 32, tin="float32", ta=ta, tb=tb)
+    assert "gemm_f32x3_f32_64x64" in plan.describe()
+    plan = run_case(dev, 2048, 2048, 96, tin="float32", ta=ta, tb=tb,
+                    alpha=0.5, beta=1.0)
+    assert "gemm_f32x3_f32_128x128" in plan.describe()
+    plan = run_case(dev, 128, 64, 160, batch=3, pad=4, tin="float32", ta=ta,
+                    tb=tb, epilogue=Epilogue.kBiasThenGELUWithAux,
+                    separate_c=True, beta=0.25)
+    assert "gemm_f32x3" in plan.describe()
+
+
+def test_f32_split_kernel_special_values(dev):
+    """Infinities and NaNs reach the output as in an f32 product: the
+    split keeps an infinite element whole in its leading part."""
+    m = n = k = 64
+    a = torch.ones(m, k, dtype=torch.float32, device=dev)
+    b = torch.full((k, n), 0.5, dtype=torch.float32, device=dev)
+    a[3, 5] = float("inf")
+    a[7, 1] = float("-inf")
+    b[2, 9] = float("nan")
+    a[10, 0] = 3.4e38  # near the f32 maximum: the parts must stay finite
+    a[11, 4] = float("nan")
+    lay = lambda r, c: MatrixLayout("float32", r, c)
+    plan = BlasLt.get_matmul_plan(
+        GemmConfig(lay(m, k), lay(k, n), lay(m, n), lay(m, n)),
+        Epilogue.kDefault)
+    d = torch.empty(m, n, dtype=torch.float32, device=dev)
+    plan.execute_on_stream(None, MemoryArgs(a, b, None, d))
+    torch.cuda.synchronize()
+    assert "gemm_f32x3" in plan.describe()
+    want = a.double().cpu().numpy() @ b.double().cpu().numpy()
+    got = d.cpu().numpy().astype(np.float64)
+    fin = np.isfinite(want)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isposinf(got), np.isposinf(want))
+    assert np.array_equal(np.isneginf(got), np.isneginf(want))
+    assert np.allclose(got[fin], want[fin], rtol=1e-6, atol=0)
