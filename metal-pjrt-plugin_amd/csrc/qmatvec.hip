@@ -920,7 +920,6 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_i8_kernel(QmvArgs a) {
     if (c < XV) xl[c] = xraw[q];
   }
   __syncthreads();
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   // The lane's x: chunk 64 j + l covers x[16 (64 j + l) ...], two vectors.
   u32x4 xr[CPL][2];
 #pragma unroll
@@ -995,6 +994,33 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_i8_kernel(QmvArgs a) {
   int row = gw;
   static_assert(D == 2 || D % 4 == 0, "rows are reduced four at a time");
   constexpr int DA = D < 4 ? 4 : D;
+  // Reduce one round's partial sums and store rows row + d GW < N.
+  auto finish = [&](const float (&acc)[DA]) {
+    if (row + GW >= a.n) {
+      const float v = wave_sum_dpp(acc[0]);
+      if (lane == 0) Y[row] = from_f32<bf16>(v);
+    } else {
+#pragma unroll
+      for (int q = 0; q < DA; q += 4) {
+        const float v = wave_sum4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3],
+                                  lane);
+        const int rr = row + (q + (lane & 3)) * GW;
+        if (lane < 4 && q + lane < D && rr < a.n) Y[rr] = from_f32<bf16>(v);
+      }
+    }
+  };
+  if (row + D * GW >= a.n) {
+    // All of this wave's rows are in its first slots (one round): each row
+    // is computed as soon as its own loads have landed.
+    float acc[DA] = {};
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (row + d * GW < a.n) acc[d] = row_acc(buf[d]);
+    finish(acc);
+    return;
+  }
+  // The loop below starts from "nothing outstanding" (as in qmv_m1_kernel).
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   for (; row + (2 * D - 1) * GW < a.n; row += D * GW) {
     float acc[DA] = {};
 #pragma unroll
@@ -1020,18 +1046,7 @@ __global__ __launch_bounds__(kStreamThreads) void qmv_m1_i8_kernel(QmvArgs a) {
         if (nr < a.n) load_row(nr, buf[d]);
       }
     }
-    if (row + GW >= a.n) {
-      const float v = wave_sum_dpp(acc[0]);
-      if (lane == 0) Y[row] = from_f32<bf16>(v);
-    } else {
-#pragma unroll
-      for (int q = 0; q < DA; q += 4) {
-        const float v = wave_sum4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3],
-                                  lane);
-        const int rr = row + (q + (lane & 3)) * GW;
-        if (lane < 4 && q + lane < D && rr < a.n) Y[rr] = from_f32<bf16>(v);
-      }
-    }
+    finish(acc);
   }
 }
 
@@ -1058,6 +1073,19 @@ int M1DepthForced() {
   return d;
 }
 
+// Workgroups per CU for the M = 1 kernels: the fewest (2..6) for which
+// every wave's rows fit its first `depth` slots (one round: each row is
+// then computed as soon as it lands, none waits for a ring refill), else
+// 2. Measured at 12288 x 4096: 6 per CU (one round) 6.9 us int4 and
+// 10.7 us int8 against 7.2 and 11.0 us with 2 (three rounds); where 2
+// already give one round (4096 rows), more workgroups only cost.
+int SingleRoundWgPerCu(int n, int cus, int depth) {
+  const int waves = kStreamThreads / 64;
+  for (int wg = 2; wg <= 6; ++wg)
+    if (static_cast<int64_t>(cus) * wg * waves * depth >= n) return wg;
+  return 2;
+}
+
 template <int PACK>
 bool LaunchM1(const QmvArgs& a, int cus, hipStream_t stream, qk_status* st) {
   const int cpr = a.row_bytes / 16;
@@ -1073,7 +1101,8 @@ bool LaunchM1(const QmvArgs& a, int cus, hipStream_t stream, qk_status* st) {
   // workgroups per CU with two rows per wave. Measured on MI355X at the
   // Qwen3-8B decode shapes, this beats full occupancy by 10-20%.
   const bool deep = cpl == 2 && a.n >= 32768;
-  const int dflt_wg = deep ? 1 : 2, dflt_depth = deep ? 4 : 2;
+  const int dflt_depth = deep ? 4 : 2;
+  const int dflt_wg = deep ? 1 : SingleRoundWgPerCu(a.n, cus, dflt_depth);
   auto go = [&](auto kernel) {
     const int resident = ResidentBlocks(reinterpret_cast<const void*>(kernel),
                                         kStreamThreads, lds);
@@ -1117,7 +1146,9 @@ bool LaunchM1I8(const QmvArgs& a, int cus, hipStream_t stream, qk_status* st) {
   auto go = [&](auto kernel) {
     const int resident = ResidentBlocks(reinterpret_cast<const void*>(kernel),
                                         kStreamThreads, lds);
-    const int per_cu = std::min(QmvWgPerCu() ? QmvWgPerCu() : 2, resident);
+    const int per_cu = std::min(
+        QmvWgPerCu() ? QmvWgPerCu() : SingleRoundWgPerCu(a.n, cus, 2),
+        resident);
     const int grid = std::max(1, std::min(need, cus * per_cu));
     kernel<<<grid, kStreamThreads, lds, stream>>>(a);
     *st = PostLaunch("qmv_m1_i8");
