@@ -675,6 +675,282 @@ qmm_ws_kernel(SkArgs a) {
   }
 }
 
+// The persistent form of qmm_ws_kernel for int4, one block of 16 rows of
+// x, K <= 4096 and more row blocks of 48 weight rows than CUs (the
+// lm_head). One workgroup per CU walks row blocks blockIdx.x, blockIdx.x
+// + gridDim.x, ...; consumer c takes K ranges (items of four groups) c and
+// c + 8 of every row block, so it keeps their x fragments in registers
+// after the first row block and only the first row block's items carry x
+// (x is read once per workgroup, not once per row block). Per row block,
+// each consumer writes its partial tile into one of two LDS buffers and
+// counts itself in with an LDS atomic; the last one sums the partials and
+// stores, then marks the buffer reusable (done[b]), so the producers
+// never wait for a reduction. Hand-off, producers and bounded spins as in
+// qmm_ws_kernel. Measured at 151936 x 4096: 94 us against 108 us for the
+// register-staged kernel at M = 16, 98 against 107 at M = 8.
+constexpr int kWspConsumers = 8;
+
+// s_waitcnt vmcnt(n) for a run-time n in [LO, HI], as a branch tree over
+// immediates (the count is an instruction field).
+template <int LO, int HI>
+__device__ __forceinline__ void WaitVmcnt(int n) {
+  if constexpr (LO == HI) {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LO) : "memory");
+  } else {
+    constexpr int MID = (LO + HI) / 2;
+    if (n <= MID)
+      WaitVmcnt<LO, MID>(n);
+    else
+      WaitVmcnt<MID + 1, HI>(n);
+  }
+}
+
+__global__ __launch_bounds__((kWspConsumers + kWsProducers) * 64) void
+qmm_wsp_kernel(SkArgs a) {
+  constexpr int NC = kWspConsumers, NP = kWsProducers, NB = 3;
+  constexpr int NR = 16 * NB;                  // weight rows per block
+  constexpr int TS = NR + 4;                   // partial-tile row stride
+  constexpr int kCDma = NR * 128 / 1024;       // 6
+  constexpr int kSDma = (NR * 2 + 63) / 64;    // 2
+  constexpr int kCOff = 8192, kSOff = kCOff + kCDma * 1024,
+                kBOff = kSOff + kSDma * 256;
+  constexpr int kSlot = kBOff + kSDma * 256;
+  constexpr int kDmaW = kCDma + 2 * kSDma;     // a weight item's DMA
+  constexpr int kDmaX = kDmaW + 8;             // with its x
+  constexpr int kFly = 3;
+  constexpr int kPart = NC * 16 * TS;          // floats per buffer
+  constexpr int S = (160 * 1024 - 2 * kPart * 4 - 512) / kSlot;
+  static_assert(kFly * kDmaX <= 63, "memory counter");
+  static_assert(S >= NP * kFly + 1, "ring depth");
+  __shared__ __attribute__((aligned(16))) unsigned char ring[S * kSlot];
+  __shared__ __attribute__((aligned(16))) float part[2][kPart];
+  __shared__ uint32_t flags[2 * S + 4];  // ready[S], freed[S], cnt[2], done[2]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int G = a.groups;
+  const int J = G / 4;  // K ranges per row block, <= 2 NC
+  const int nrb = (a.n + NR - 1) / NR;
+  const int rbs = (nrb - static_cast<int>(blockIdx.x) +
+                   static_cast<int>(gridDim.x) - 1) / gridDim.x;
+  const int T = rbs * J;  // items
+  uint32_t* const ready = flags;
+  uint32_t* const freed = flags + S;
+  uint32_t* const cnt = flags + 2 * S;
+  uint32_t* const done = flags + 2 * S + 2;
+  if (threadIdx.x < 2 * S + 4) LdsStoreVolatile(flags + threadIdx.x, 0);
+  __syncthreads();
+  auto block_n0 = [&](int i) {
+    return (static_cast<int>(blockIdx.x) + i * static_cast<int>(gridDim.x)) *
+           NR;
+  };
+  // A spin of at most 2^20 polls (~70 ms): a wave that waits longer gives
+  // up and goes on (wrong results, but the kernel ends).
+  auto spin_until = [](const uint32_t* f, uint32_t want) {
+    for (int it = 0; it < (1 << 20); ++it) {
+      if (__builtin_amdgcn_readfirstlane(LdsLoadVolatile(f)) == want) return;
+      __builtin_amdgcn_s_sleep(1);
+    }
+  };
+
+  if (wave >= NC) {
+    // Producer p = wave - NC moves items p, p + NP, ...; item t is K range
+    // t % J of row block t / J; the first row block's items carry x. Lane
+    // maps as in qmm_ws_kernel.
+    const int p = wave - NC;
+    const int row_bytes = a.k / 2;
+    DmaRsrc crs, xrs, srs, brs;
+    crs.make(a.codes, static_cast<long long>(a.n) * row_bytes);
+    xrs.make(a.x, static_cast<long long>(a.m) * a.k * 2);
+    srs.make(a.scales, static_cast<long long>(a.n) * G * 2);
+    brs.make(a.biases, a.has_bias ? static_cast<long long>(a.n) * G * 2 : 0);
+    int xvo[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 2 * i + lane / 32, q = lane % 32;
+      xvo[i] = (r * a.k + ((q & ~7) | ((q & 7) ^ (r & 7))) * 8) * 2;
+    }
+    auto publish = [&](int t) {
+      if (lane == 0) LdsStoreVolatile(ready + t % S, t + 1);
+    };
+    int issued = 0, published = 0;  // own items
+    for (int t = p; t < T; t += NP) {
+      const int s = t % S;
+      unsigned char* slot = ring + s * kSlot;
+      if (t >= S && __builtin_amdgcn_readfirstlane(LdsLoadVolatile(
+                        freed + s)) != static_cast<uint32_t>(t - S + 1)) {
+        // Publish everything in flight before waiting: a consumer of one
+        // of those items may be what frees the slot.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        for (; published < issued; ++published) publish(p + NP * published);
+        spin_until(freed + s, t - S + 1);
+      }
+      const int n0 = block_n0(t / J);
+      const int g = 4 * (t % J);
+#pragma unroll
+      for (int i = 0; i < kCDma; ++i) {
+        const int rr = 8 * i + lane / 8, r = n0 + rr;
+        const int vo =
+            r < a.n ? r * row_bytes + (((lane % 8) ^ ((rr >> 1) & 7)) << 4)
+                    : kOut;
+        crs.dma_nt(slot + kCOff + i * 1024, vo, g * 32);
+      }
+#pragma unroll
+      for (int i = 0; i < kSDma; ++i) {
+        const int rr = (64 * i + lane) / 2, r = n0 + rr;
+        const int vo = (rr < NR && r < a.n)
+                           ? r * G * 2 + ((64 * i + lane) % 2) * 4
+                           : kOut;
+        srs.dma4(slot + kSOff + i * 256, vo, g * 2);
+        brs.dma4(slot + kBOff + i * 256, vo, g * 2);
+      }
+      if (t < J) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xrs.dma(slot + i * 1024, xvo[i], g * 128);
+      }
+      ++issued;
+      if (issued - published >= kFly) {
+        // The oldest own item in flight has landed once only the DMA of
+        // the kFly - 1 newer ones is outstanding.
+        int newer = 0;
+#pragma unroll
+        for (int d = 1; d < kFly; ++d)
+          newer += p + NP * (published + d) < J ? kDmaX : kDmaW;
+        WaitVmcnt<0, 63>(newer);
+        publish(p + NP * published);
+        ++published;
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    for (; published < issued; ++published) publish(p + NP * published);
+    return;
+  }
+
+  // Consumer.
+  const int q16 = lane >> 4, l16 = lane & 15;
+  const uint32_t kMask = vgpr_const(0x000F000Fu);
+  const uint32_t kBias = vgpr_const(0x43004300u);
+  const bf16x8 ones = __builtin_bit_cast(
+      bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  bf16x8 xk[2][4][2];  // x fragments of K ranges wave and wave + NC
+  for (int i = 0; i < rbs; ++i) {
+    f32x4 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int j = wave + u * NC;
+      if (j >= J) continue;
+      const int t = i * J + j;
+      const int s = t % S;
+      const unsigned char* slot = ring + s * kSlot;
+      spin_until(ready + s, t + 1);
+      asm volatile("" ::: "memory");  // the slot's reads stay below
+      if (i == 0) {
+        // the lane's x chunks 2 (l / 16) and 2 (l / 16) + 1 of row l % 16
+        // for each group, as code-word pairs
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            xk[u][gg][h] = XPairs(*reinterpret_cast<const u32x4*>(
+                slot + l16 * 512 +
+                ((8 * gg + ((2 * q16 + h) ^ (l16 & 7))) << 4)));
+      }
+      u32x2 wv[4][NB];
+      uint32_t sv[2][NB], bv[2][NB];
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int r = 16 * nb + l16;
+          const int c = 2 * gg + (q16 >> 1);
+          wv[gg][nb] = *reinterpret_cast<const u32x2*>(
+              slot + kCOff + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) +
+              ((q16 & 1) << 3));
+        }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int r = 16 * nb + l16;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          sv[h][nb] =
+              *reinterpret_cast<const uint32_t*>(slot + kSOff + r * 8 + 4 * h);
+          bv[h][nb] =
+              *reinterpret_cast<const uint32_t*>(slot + kBOff + r * 8 + 4 * h);
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (lane == 0) LdsStoreVolatile(freed + s, t + 1);
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg) {
+        f32x4 xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            xk[u][gg][0], ones, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xk[u][gg][1], ones, xs,
+                                                     0, 0, 0);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              xk[u][gg][0], CodePairs(wv[gg][nb][0], kMask, kBias),
+              f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              xk[u][gg][1], CodePairs(wv[gg][nb][1], kMask, kBias), tmp, 0,
+              0, 0);
+          const int sh = 16 * (gg & 1);
+          const float sc = __uint_as_float((sv[gg >> 1][nb] >> sh) << 16);
+          const float of = __uint_as_float((bv[gg >> 1][nb] >> sh) << 16);
+          const float off = of - 128.f * sc;  // codes enter as q + 128
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[nb][r] = fmaf(sc, tmp[r], fmaf(off, xs[r], acc[nb][r]));
+        }
+      }
+    }
+
+    // Row block i: partial tile into buffer b (free once block i - 2 has
+    // been summed), count in; the last consumer sums and stores.
+    const int b = i & 1;
+    if (i >= 2) spin_until(done + b, i - 1);
+    float* const pb = part[b];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        pb[(wave * 16 + 4 * q16 + r) * TS + 16 * nb + l16] = acc[nb][r];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    uint32_t old = 0;
+    if (lane == 0)
+      old = __hip_atomic_fetch_add(cnt + b, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+    old = __builtin_amdgcn_readfirstlane(old);
+    asm volatile("" ::: "memory");  // the partial tiles' reads stay below
+    if (old == NC - 1) {
+      // four consecutive columns per lane and step
+      const int n0 = block_n0(i);
+      bf16* Y = static_cast<bf16*>(a.y);
+      for (int e = lane; e < 4 * NR; e += 64) {
+        const int r = e / (NR / 4), c = 4 * (e % (NR / 4));
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < NC; ++w)
+          v += *reinterpret_cast<const f32x4*>(pb + (w * 16 + r) * TS + c);
+        if (r < a.m) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (n0 + c + q < a.n)
+              Y[static_cast<long long>(r) * a.n + n0 + c + q] =
+                  from_f32<bf16>(v[q]);
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (lane == 0) {
+        LdsStoreVolatile(cnt + b, 0);
+        LdsStoreVolatile(done + b, i + 1);
+      }
+    }
+  }
+}
+
 }  // namespace
 
 bool QSkinnyApplies(const QuantProblem& p) {
@@ -752,6 +1028,15 @@ qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream) {
     }
 #undef QK_WS
     return PostLaunch("qmm_ws");
+  }
+  // The persistent form for the int4 shapes with more 48-row blocks than
+  // CUs (the lm_head) and K <= 4096.
+  if (int4 && mb == 1 && !ws_off && ws_nb == 0 && a.groups % 4 == 0 &&
+      a.groups / 4 <= 2 * kWspConsumers) {
+    const int nrb = (a.n + 47) / 48;
+    qmm_wsp_kernel<<<std::min(nrb, cus),
+                     (kWspConsumers + kWsProducers) * 64, 0, stream>>>(a);
+    return PostLaunch("qmm_wsp");
   }
   const int cg = int4 && mb <= 2 ? 4 : 2;
   bool wide = (a.n + 31) / 32 >= cus && mb <= (int4 ? 2 : 1);

@@ -121,6 +121,7 @@ def test_qmatvec_single_row_paths(dev, packing, k):
 @pytest.mark.parametrize("mnk", [(5, 300, 4096), (8, 77, 1024),
                                  (16, 4096, 4096), (16, 6000, 1024),
                                  (12, 9000, 3072), (16, 12400, 1024),
+                                 (7, 12500, 4096), (9, 12400, 5120),
                                  (32, 1000, 512), (27, 9000, 2048),
                                  (33, 64, 1024), (40, 520, 12288),
                                  (64, 2048, 2048)])
@@ -133,8 +134,9 @@ def test_qmatvec_few_rows(dev, mnk, packing):
     offsets, elementwise against the float64 oracle. For int4 and at most
     16 rows: the streamed kernel with 16, 32 and 48 weight rows per
     workgroup (N = 4096, 6000, 9000; the last two with a partly filled
-    workgroup) and the register-staged one with 48 (N = 12400, more
-    workgroups than CUs), K of 4, 12 and 64 items of four groups; for
+    workgroup), its persistent form where 48-row blocks outnumber the CUs
+    and K <= 4096 (N = 12400, 12500; K of 4 and 16 items of four groups)
+    and the register-staged kernel beyond (K = 5120); for
     int4 and 17..32 rows the streamed kernel with two row blocks of x
     (M = 32, 27)."""
     m, n, k = mnk
