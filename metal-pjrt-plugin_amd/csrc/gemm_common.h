@@ -481,7 +481,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs g) {
 //
 // Buffer descriptors take a 32-bit extent, so each operand of one batch
 // entry must span less than 2^31 bytes (checked by the launcher).
-template <typename T, int R, int BK, int NT, bool KCONT>
+// VCHK: the whole offset goes in the vector offset, which the descriptor's
+// extent checks (rows past the extent read zeros).
+template <typename T, int R, int BK, int NT, bool KCONT, bool VCHK = false>
 struct BufferLoader {
   static constexpr int VPR = (KCONT ? BK : R) / 8;  // vectors per source row
   static constexpr int RPI = NT / VPR;  // source rows between vector slots
@@ -505,7 +507,10 @@ struct BufferLoader {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int soff = (base + i * RPI * ld) * static_cast<int>(sizeof(T));
-      v[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, 0);
+      if constexpr (VCHK)
+        v[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff + soff, 0, 0);
+      else
+        v[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, 0);
     }
   }
   __device__ __forceinline__ void store(T* lds, int tid) const {
@@ -525,7 +530,9 @@ struct BufferLoader {
 // output type and activation are template arguments, chosen once by
 // store_direct, so the per-element code has no branches on them.
 // Arithmetic order as store_tile: alpha*acc, + beta*C, + bias.
-template <typename O, int ACT, int BM, int BN, int WM, int WN>
+// MC: rows at or past g.m are neither read (C) nor written (the last M
+// tile of a kernel whose M need not be a multiple of BM).
+template <typename O, int ACT, int BM, int BN, int WM, int WN, bool MC>
 __device__ __forceinline__ void store_direct_t(
     const GemmArgs& g, const f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
     int m0, int n0, long long batch, int lane, int wm, int wn) {
@@ -555,12 +562,16 @@ __device__ __forceinline__ void store_direct_t(
       auto at = [&](int r) {
         return base + static_cast<long long>(8 * (r >> 2) + (r & 3)) * g.ldd;
       };
+      auto live = [&](int r) {
+        return !MC || rowb + i * 32 + 8 * (r >> 2) + (r & 3) < g.m;
+      };
       float v[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) v[r] = g.alpha * acc[i][j][r];
       if (g.use_c) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] += g.beta * to_f32(C[at(r)]);
+        for (int r = 0; r < 16; ++r)
+          if (live(r)) v[r] += g.beta * to_f32(C[at(r)]);
       }
       if (g.has_bias) {
 #pragma unroll
@@ -568,14 +579,16 @@ __device__ __forceinline__ void store_direct_t(
       }
       if (g.has_aux) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) aux[at(r)] = from_f32<O>(v[r]);
+        for (int r = 0; r < 16; ++r)
+          if (live(r)) aux[at(r)] = from_f32<O>(v[r]);
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) D[at(r)] = from_f32<O>(act_f32(ACT, v[r]));
+      for (int r = 0; r < 16; ++r)
+        if (live(r)) D[at(r)] = from_f32<O>(act_f32(ACT, v[r]));
     }
 }
 
-template <typename T, int BM, int BN, int WM, int WN>
+template <typename T, int BM, int BN, int WM, int WN, bool MC = false>
 __device__ __forceinline__ void store_direct(
     const GemmArgs& g, const f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
     int m0, int n0, long long batch, int lane, int wm, int wn) {
@@ -583,23 +596,31 @@ __device__ __forceinline__ void store_direct(
     using O = decltype(out);
     switch (g.act) {
       case 1:
-        return store_direct_t<O, 1, BM, BN, WM, WN>(g, acc, m0, n0, batch, lane, wm, wn);
+        return store_direct_t<O, 1, BM, BN, WM, WN, MC>(g, acc, m0, n0, batch, lane, wm, wn);
       case 2:
-        return store_direct_t<O, 2, BM, BN, WM, WN>(g, acc, m0, n0, batch, lane, wm, wn);
+        return store_direct_t<O, 2, BM, BN, WM, WN, MC>(g, acc, m0, n0, batch, lane, wm, wn);
       case 3:
-        return store_direct_t<O, 3, BM, BN, WM, WN>(g, acc, m0, n0, batch, lane, wm, wn);
+        return store_direct_t<O, 3, BM, BN, WM, WN, MC>(g, acc, m0, n0, batch, lane, wm, wn);
       default:
-        return store_direct_t<O, 0, BM, BN, WM, WN>(g, acc, m0, n0, batch, lane, wm, wn);
+        return store_direct_t<O, 0, BM, BN, WM, WN, MC>(g, acc, m0, n0, batch, lane, wm, wn);
     }
   };
   if (g.out_f32) go(0.f);
   else go(T{});
 }
 
-template <typename T, int BN, bool TA, class BSrc, int NW = 4, int BM = 256>
+// MC: M need not be a multiple of BM (A rows past M read zeros through the
+// descriptor's extent, output rows past M are not stored); AK only.
+// DEPTH = 2 keeps two register sets of operand loads in flight, so a
+// tile's loads are issued two K tiles of MFMA work before they are stored
+// to LDS (for small tiles whose K step is shorter than the load latency).
+template <typename T, int BN, bool TA, class BSrc, int NW = 4, int BM = 256,
+          int DEPTH = 1, bool MC = false>
 __global__ __launch_bounds__(NW * 64) void gemm_fast_kernel(GemmArgs g) {
   constexpr int BK = 64, NT = NW * 64, WM = NW / 2, WN = 2;
   static_assert(BSrc::NT == NT, "B loader built for this workgroup");
+  static_assert(DEPTH == 1 || DEPTH == 2, "one or two register sets");
+  static_assert(!MC || !TA, "row bounds through the extent of a K-contiguous A");
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
   constexpr bool AK = !TA, BKC = BSrc::kKCont;  // K-contiguous operands
   using LA = TileLayout<T, BM, BK, AK>;
@@ -623,11 +644,12 @@ __global__ __launch_bounds__(NW * 64) void gemm_fast_kernel(GemmArgs g) {
   const int m0 = tm * BM, n0 = tn * BN;
   const long long batch = blockIdx.y;
 
-  BufferLoader<T, BM, BK, NT, AK> la;
-  la.init(static_cast<const T*>(g.a) + batch * g.bsa,
-          static_cast<long long>(AK ? g.m : g.k) * g.lda * sizeof(T), g.lda,
-          tid);
-  BSrc lb(g, batch, tid);
+  BufferLoader<T, BM, BK, NT, AK, MC> la0, la1;
+  la0.init(static_cast<const T*>(g.a) + batch * g.bsa,
+           static_cast<long long>(AK ? g.m : g.k) * g.lda * sizeof(T), g.lda,
+           tid);
+  if constexpr (DEPTH == 2) la1 = la0;
+  BSrc lb0(g, batch, tid), lb1 = lb0;
 
   f32x16 acc[FM][FN];
 #pragma unroll
@@ -638,10 +660,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_fast_kernel(GemmArgs g) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int ktiles = g.k / BK;  // >= 1
-  la.load(m0, 0);
-  lb.load(n0, 0);
-  la.store(lds_a(0), tid);
-  lb.store(lds_b(0), tid);
+  la0.load(m0, 0);
+  lb0.load(n0, 0);
+  la0.store(lds_a(0), tid);
+  lb0.store(lds_b(0), tid);
   __syncthreads();
   typename Frag<T>::type fa[2][FM], fb[2][FN];
 #pragma unroll
@@ -650,14 +672,16 @@ __global__ __launch_bounds__(NW * 64) void gemm_fast_kernel(GemmArgs g) {
 #pragma unroll
   for (int j = 0; j < FN; ++j)
     fb[0][j] = load_frag<T, BN, BK, BKC>(lds_b(0), wn * WTN + j * 32, 0, lane);
-  {
-    const int k1 = min(1, ktiles - 1) * BK;
-    la.load(m0, k1);
-    lb.load(n0, k1);
+  // Register set (t - 1) % DEPTH holds tile t.
+  la0.load(m0, min(1, ktiles - 1) * BK);
+  lb0.load(n0, min(1, ktiles - 1) * BK);
+  if constexpr (DEPTH == 2) {
+    la1.load(m0, min(2, ktiles - 1) * BK);
+    lb1.load(n0, min(2, ktiles - 1) * BK);
   }
   // DS reads per K step (a transposing fragment read is two instructions).
   constexpr int kReads = FM * (AK ? 1 : 2) + FN * (BKC ? 1 : 2);
-  for (int kt = 0; kt < ktiles; ++kt) {
+  auto step = [&](int kt, auto& la, auto& lb) {
     const int cur = kt & 1;
 #pragma unroll
     for (int s = 0; s < BK / 16; ++s) {
@@ -681,10 +705,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_fast_kernel(GemmArgs g) {
         // was the previous tile, which ended on a barrier.
         la.store(lds_a(cur ^ 1), tid);
         lb.store(lds_b(cur ^ 1), tid);
-        // The registers are free again: request the tile after next right
-        // away, a whole tile of MFMA work before it is needed (requesting
-        // it after the barrier gave ~16% less at 4096^3).
-        const int k2 = min(kt + 2, ktiles - 1) * BK;
+        // The registers are free again: request the tile DEPTH + 1 ahead
+        // right away (requesting it after the barrier gave ~16% less at
+        // 4096^3 with one set).
+        const int k2 = min(kt + 1 + DEPTH, ktiles - 1) * BK;
         la.load(m0, k2);
         lb.load(n0, k2);
       }
@@ -707,8 +731,16 @@ __global__ __launch_bounds__(NW * 64) void gemm_fast_kernel(GemmArgs g) {
     for (int j = 0; j < FN; ++j)
       fb[0][j] = load_frag<T, BN, BK, BKC>(lds_b(cur ^ 1), wn * WTN + j * 32,
                                            0, lane);
+  };
+  if constexpr (DEPTH == 1) {
+    for (int kt = 0; kt < ktiles; ++kt) step(kt, la0, lb0);
+  } else {
+    for (int kt = 0; kt < ktiles; kt += 2) {
+      step(kt, la0, lb0);
+      if (kt + 1 < ktiles) step(kt + 1, la1, lb1);
+    }
   }
-  store_direct<T, BM, BN, WM, WN>(g, acc, m0, n0, batch, lane, wm, wn);
+  store_direct<T, BM, BN, WM, WN, MC>(g, acc, m0, n0, batch, lane, wm, wn);
 }
 
 

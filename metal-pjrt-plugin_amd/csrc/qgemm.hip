@@ -238,28 +238,31 @@ struct QuantFastB {
                   ? static_cast<float>(static_cast<int8_t>(word & 255u))
                   : static_cast<float>(word & 255u);
         }
-        o.e[j] = from_f32<T>(__fadd_rn(__fmul_rn(q, sc), bi));
+        // q * sc is exact in f32 (at most 8 + 8 significant bits), so
+        // the fused form rounds exactly as the unfused canonical one.
+        o.e[j] = from_f32<T>(fmaf(q, sc, bi));
       }
       *reinterpret_cast<u32x4*>(dst + 8 * v) = o.u;
     }
   }
 };
 
-// The interior-tile kernel for M a multiple of 128, N of 128, group 64,
-// bf16 scales/offsets; false when it does not apply. Eight waves; tiles
-// of 256 x 256, 256 x 128 or 128 x 128 (two workgroups per CU), the
-// largest that leaves no CU idle.
+// The interior-tile kernel for any M, N a multiple of 128, group 64, bf16
+// scales/offsets; false when it does not apply. Eight waves; tiles of
+// 256 x 256, 256 x 128 or 128 x 128 (two workgroups per CU); the last M
+// tile may be partly filled (A rows past M read zeros, their outputs are
+// not stored).
 template <typename T, int PACK>
 bool LaunchFastQ(GemmArgs g, int m, int n, hipStream_t stream,
                  qk_status* st) {
   if constexpr (PACK == QK_PACK_BYTE_HALFSPLIT) {
     return false;
   } else {
-    if (m % 128 != 0 || n % 128 != 0 || g.k % 64 != 0 || g.k == 0 ||
+    if (m <= 0 || n % 128 != 0 || g.k % 64 != 0 || g.k == 0 ||
         g.qgroup != 64 || g.qsdt != QK_BF16 ||
         (g.qhas_bias && g.qbdt != QK_BF16) ||
         static_cast<int64_t>(n) * g.qrow_bytes >= (int64_t{1} << 31) ||
-        static_cast<int64_t>(m) * g.k * 2 >= (int64_t{1} << 31) ||
+        (static_cast<int64_t>(m) + 256) * g.k * 2 >= (int64_t{1} << 31) ||
         reinterpret_cast<uintptr_t>(g.a) % 16 != 0 ||
         reinterpret_cast<uintptr_t>(g.b) % 16 != 0)
       return false;
@@ -274,10 +277,10 @@ bool LaunchFastQ(GemmArgs g, int m, int n, hipStream_t stream,
     // M = 2048: 271 / 259 / 382 (256x256 / 256x128 / 128x128). The
     // smallest tile whose count still fits one round of CUs; when none
     // does, the fewest rounds times tile size (ties to the larger tile).
-    const bool ok[4] = {false, m % 256 == 0 && n % 256 == 0, m % 256 == 0,
-                        true};
-    const long long count[4] = {0, (m / 256LL) * (n / 256),
-                                (m / 256LL) * (n / 128), (m / 128LL) * (n / 128)};
+    const long long m256 = (m + 255) / 256, m128 = (m + 127) / 128;
+    const bool ok[4] = {false, n % 256 == 0, true, true};
+    const long long count[4] = {0, m256 * (n / 256), m256 * (n / 128),
+                                m128 * (n / 128)};
     const double size[4] = {0, 1.0, 0.5, 0.25};
     int tile = 0;
     for (int t = 1; t <= 3; ++t)
@@ -292,18 +295,21 @@ bool LaunchFastQ(GemmArgs g, int m, int n, hipStream_t stream,
     }
     if (forced >= 1 && forced <= 3 && ok[forced]) tile = forced;
     const int bm = tile == 3 ? 128 : 256, bn = tile == 1 ? 256 : 128;
-    g.tiles_m = m / bm;
+    g.tiles_m = (m + bm - 1) / bm;
     g.tiles_n = n / bn;
     const dim3 grid(g.tiles_m * g.tiles_n);
+    // Two register sets of loads in flight (int8 codes in two sets would
+    // spill at 256 x 256).
     if (tile == 1)
-      gemm_fast_kernel<T, 256, false, QuantFastB<PACK, T, 256, 512>, 8>
+      gemm_fast_kernel<T, 256, false, QuantFastB<PACK, T, 256, 512>, 8, 256,
+                       PACK == QK_PACK_U32X8 ? 2 : 1, true>
           <<<grid, 512, 0, stream>>>(g);
     else if (tile == 2)
-      gemm_fast_kernel<T, 128, false, QuantFastB<PACK, T, 128, 512>, 8>
-          <<<grid, 512, 0, stream>>>(g);
+      gemm_fast_kernel<T, 128, false, QuantFastB<PACK, T, 128, 512>, 8, 256,
+                       2, true><<<grid, 512, 0, stream>>>(g);
     else
-      gemm_fast_kernel<T, 128, false, QuantFastB<PACK, T, 128, 512>, 8, 128>
-          <<<grid, 512, 0, stream>>>(g);
+      gemm_fast_kernel<T, 128, false, QuantFastB<PACK, T, 128, 512>, 8, 128,
+                       2, true><<<grid, 512, 0, stream>>>(g);
     *st = PostLaunch("qgemm_fast");
     return true;
   }

@@ -214,6 +214,34 @@ def test_qmatvec_prefill_tiles(dev, case):
                      O.round_to(w, xdt))
 
 
+@pytest.mark.parametrize("case", [
+    (2000, 8192, 128, Packing.U32X8, "bfloat16"),  # 256 x 256, 208-row tail
+    (1100, 4096, 128, Packing.U8, "bfloat16"),     # 256 x 128, 76-row tail
+    (300, 1024, 512, Packing.S8_SYM, "float16"),   # 128 x 128, 44-row tail
+    (129, 256, 256, Packing.U32X8, "bfloat16"),    # 128 x 128, one-row tail
+])
+def test_qmatvec_prefill_ragged_rows(dev, case):
+    """Row counts that are not multiples of the interior-tile GEMM's tile
+    height: the last M tile is partly filled (x rows past M read as zeros,
+    their outputs are not stored). The output is a view into a larger
+    buffer whose rows past M must keep their sentinel."""
+    m, n, k, packing, xdt = case
+    rng = np.random.default_rng(m + 3 * n + k)
+    for has_bias in (True, False):
+        dc, ds, db, w, *_ = make_weights(rng, n, k, packing, 64,
+                                         has_bias=has_bias)
+        x = O.round_to(rng.standard_normal((m, k)), xdt).astype(np.float32)
+        big = torch.full((m + 300, n), 7.0, dtype=TORCH[xdt], device=dev)
+        y = qkern.qmatvec(torch.from_numpy(x).to(TORCH[xdt]).to(dev),
+                          dc.to(dev), ds.to(dev),
+                          None if db is None else db.to(dev),
+                          packing=packing, out=big[:m])
+        torch.cuda.synchronize()
+        assert bool((big[m:] == 7.0).all()), "rows past M were written"
+        check_matvec(y.float().cpu().numpy().astype(np.float64), x,
+                     O.round_to(w, xdt))
+
+
 def test_qmatvec_leading_dims_and_no_bias(dev):
     rng = np.random.default_rng(5)
     dc, ds, _, w, *_ = make_weights(rng, 40, 256, Packing.U32X8, 64,
