@@ -273,19 +273,29 @@ qk_status DispatchTile(const GemmArgs& g, int batch, bool ta, bool tb,
   return PostLaunch(name);
 }
 
+template <typename T, int BN, int NW = 4, bool MC = false>
+qk_status DispatchFastM(const GemmArgs& g, int batch, bool ta, bool tb,
+                        hipStream_t stream, const char* name) {
+  dim3 grid(g.tiles_m * g.tiles_n, batch);
+  if (!ta && !tb)
+    gemm_dma_kernel<T, BN, false, false, NW, MC><<<grid, NW * 64, 0, stream>>>(g);
+  else if (!ta && tb)
+    gemm_dma_kernel<T, BN, false, true, NW, MC><<<grid, NW * 64, 0, stream>>>(g);
+  else if (ta && !tb)
+    gemm_dma_kernel<T, BN, true, false, NW, MC><<<grid, NW * 64, 0, stream>>>(g);
+  else
+    gemm_dma_kernel<T, BN, true, true, NW, MC><<<grid, NW * 64, 0, stream>>>(g);
+  return PostLaunch(name);
+}
+
+// M a multiple of 256: the kernel without row checks; otherwise the last
+// M tile is partly filled.
 template <typename T, int BN, int NW = 4>
 qk_status DispatchFast(const GemmArgs& g, int batch, bool ta, bool tb,
                        hipStream_t stream, const char* name) {
-  dim3 grid(g.tiles_m * g.tiles_n, batch);
-  if (!ta && !tb)
-    gemm_dma_kernel<T, BN, false, false, NW><<<grid, NW * 64, 0, stream>>>(g);
-  else if (!ta && tb)
-    gemm_dma_kernel<T, BN, false, true, NW><<<grid, NW * 64, 0, stream>>>(g);
-  else if (ta && !tb)
-    gemm_dma_kernel<T, BN, true, false, NW><<<grid, NW * 64, 0, stream>>>(g);
-  else
-    gemm_dma_kernel<T, BN, true, true, NW><<<grid, NW * 64, 0, stream>>>(g);
-  return PostLaunch(name);
+  if (g.m % 256 == 0)
+    return DispatchFastM<T, BN, NW, false>(g, batch, ta, tb, stream, name);
+  return DispatchFastM<T, BN, NW, true>(g, batch, ta, tb, stream, name);
 }
 
 template <typename T, int BMN, int KW>
@@ -409,22 +419,26 @@ bool F32x3Applies(const GemmProblem& p, int bm, int bn) {
 }
 
 // Whether the interior-tile kernel can run the problem with a BN-wide
-// tile: M, N, K multiples of the tile, 16-byte aligned operands and leading
-// dimensions, and each operand of one batch entry under 2^31 bytes (the
-// extent of a buffer descriptor).
+// tile: N and K multiples of the tile (any M: the last M tile may be
+// partly filled), 16-byte aligned operands and leading dimensions, and
+// each operand of one batch entry, with A padded to whole 256-row tiles,
+// under 2^31 bytes (the extent of a buffer descriptor).
 bool FastApplies(const GemmProblem& p, int bn) {
-  if (p.a.dtype == QK_F32 || p.m % 256 != 0 || p.n % bn != 0 ||
-      p.k % 64 != 0 || p.k == 0)
+  if (p.a.dtype == QK_F32 || p.m == 0 || p.n % bn != 0 || p.k % 64 != 0 ||
+      p.k == 0)
     return false;
   const int vec = 16 / DTypeSize(p.a.dtype);
   const bool batched = p.batch > 1;
-  auto ok = [&](const Operand& o, int64_t rows) {
+  // elems: the largest element offset a tile can address, plus one
+  auto ok = [&](const Operand& o, int64_t elems) {
     const int64_t bs = batched ? o.batch_stride : 0;
     return reinterpret_cast<uintptr_t>(o.ptr) % 16 == 0 && o.ld % vec == 0 &&
-           bs % vec == 0 && rows * o.ld * DTypeSize(o.dtype) < (int64_t{1} << 31);
+           bs % vec == 0 && elems * DTypeSize(o.dtype) < (int64_t{1} << 31);
   };
-  return ok(p.a, p.a.transpose ? p.k : p.m) &&
-         ok(p.b, p.b.transpose ? p.n : p.k);
+  const int64_t mpad = CeilDiv(p.m, 256) * 256;
+  return ok(p.a, p.a.transpose ? (p.k - 1) * p.a.ld + mpad
+                               : mpad * p.a.ld) &&
+         ok(p.b, (p.b.transpose ? p.n : p.k) * p.b.ld);
 }
 
 GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {

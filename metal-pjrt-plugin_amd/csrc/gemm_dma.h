@@ -1,7 +1,7 @@
 // Interior-tile f16/bf16 GEMM whose operand tiles travel from global memory
 // straight into LDS (gfx950 `buffer_load_dwordx4 ... lds`), used by the
-// dense GEMM for problems whose M, N and K are multiples of 256 x BN x 64
-// (BN = 256, 192 or 128) with 16-byte aligned operands. Replaces the tiled loop
+// dense GEMM for problems whose N and K are multiples of BN x 64 (BN =
+// 256, 192 or 128; any M) with 16-byte aligned operands. Replaces the tiled loop
 // of the reference's steel GEMM (metal_pjrt/kernels/steel_gemm.metal:
 // 180-213) for those shapes; the store applies the same epilogue.
 //
@@ -46,7 +46,9 @@ namespace {
 // Operand tile of R rows x 64 K, K-contiguous in memory (row stride ld
 // elements): R / 32 DMA instructions per wave; instruction i of wave w
 // fills rows (4 i + w) * 8 .. + 8.
-template <typename T, int R, int NW = 4>
+// VC: the whole offset goes in the vector offset, which the descriptor's
+// extent checks (for tiles that run past the operand's last row).
+template <typename T, int R, int NW = 4, bool VC = false>
 struct DmaK {
   static constexpr int NI = R / (8 * NW);
   static constexpr int kBytes = R * 128;
@@ -61,8 +63,11 @@ struct DmaK {
   }
   __device__ __forceinline__ void issue(unsigned char* lds, int r0, int k0,
                                         int w, int i) const {
-    rs.dma(lds + (i * NW + w) * 1024, voff,
-           ((r0 + i * 8 * NW) * ld + k0) * static_cast<int>(sizeof(T)));
+    const int so = ((r0 + i * 8 * NW) * ld + k0) * static_cast<int>(sizeof(T));
+    if constexpr (VC)
+      rs.dma(lds + (i * NW + w) * 1024, voff + so, 0);
+    else
+      rs.dma(lds + (i * NW + w) * 1024, voff, so);
   }
   // Fragment for rows rb .. rb + 31 (rb % 32 == 0), K elements kb + 8 (lane
   // / 32) .. + 7.
@@ -79,7 +84,7 @@ struct DmaK {
 // stride ld elements): K row k occupies R * sizeof(T) bytes; a DMA
 // instruction covers RPI K rows, instruction i of wave w fills K rows
 // (4 i + w) * RPI .. + RPI.
-template <typename T, int R, int NW = 4>
+template <typename T, int R, int NW = 4, bool VC = false>
 struct DmaMN {
   static constexpr int RB = R * static_cast<int>(sizeof(T));  // row bytes
   static constexpr int LPR = RB / 16;                         // lanes per row
@@ -100,8 +105,11 @@ struct DmaMN {
   }
   __device__ __forceinline__ void issue(unsigned char* lds, int r0, int k0,
                                         int w, int i) const {
-    rs.dma(lds + (i * NW + w) * 1024, voff,
-           ((k0 + i * NW * RPI) * ld + r0) * static_cast<int>(sizeof(T)));
+    const int so = ((k0 + i * NW * RPI) * ld + r0) * static_cast<int>(sizeof(T));
+    if constexpr (VC)
+      rs.dma(lds + (i * NW + w) * 1024, voff + so, 0);
+    else
+      rs.dma(lds + (i * NW + w) * 1024, voff, so);
   }
   // Fragment for columns rb .. rb + 31 and K kb .. kb + 15 with the
   // transposing read (lane s of a 16-lane group addresses K row
@@ -166,11 +174,17 @@ constexpr int VmcntImm(int n) {
   return (n & 0xF) | (((n >> 4) & 3) << 14) | (7 << 4) | (0xF << 8);
 }
 
-template <typename T, int BN, bool TA, bool TB, int NWV = 4>
+// MC: M need not be a multiple of 256. The A tile's DMA offsets go wholly
+// in the range-checked vector offset (rows, or M-contiguous columns, past
+// the operand's extent read zeros) and the epilogue skips rows past M;
+// values fetched for rows past M (in range of the extent) only reach
+// those skipped rows.
+template <typename T, int BN, bool TA, bool TB, int NWV = 4, bool MC = false>
 __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(GemmArgs g) {
   constexpr int BM = 256, BK = 64, WN = 2, WM = NWV / WN;
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
-  using LA = std::conditional_t<TA, DmaMN<T, BM, NWV>, DmaK<T, BM, NWV>>;
+  using LA = std::conditional_t<TA, DmaMN<T, BM, NWV, MC>,
+                                DmaK<T, BM, NWV, MC>>;
   using LB = std::conditional_t<
       TB, DmaK<T, BN, NWV>,
       std::conditional_t<BN == 192, DmaMN192<T, NWV>, DmaMN<T, BN, NWV>>>;
@@ -292,7 +306,7 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(GemmArgs g) {
   if (kt < ktiles) tile(st0, st1, kt);
   // No DMA may still be writing this workgroup's LDS when it ends.
   __builtin_amdgcn_s_waitcnt(VmcntImm(0));
-  store_direct<T, BM, BN, WM, WN>(g, acc, m0, n0, batch, lane, wm, wn);
+  store_direct<T, BM, BN, WM, WN, MC>(g, acc, m0, n0, batch, lane, wm, wn);
 }
 
 }  // namespace

@@ -212,10 +212,26 @@ def test_interior_tile_kernel_epilogues(dev):
     assert "256x192" in plan.describe()
 
 
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_interior_tile_kernel_ragged_m(dev, ta, tb):
+    """M not a multiple of 256: the interior-tile kernel with a partly
+    filled last M tile (A rows past M read as zeros, output rows past M not
+    stored). Batched with packed batch entries, so a row written past M
+    would land in the next entry's output."""
+    plan = run_case(dev, 2000, 2048, 128, ta=ta, tb=tb)
+    assert "gemm_fast_bf16" in plan.describe()
+    plan = run_case(dev, 1000, 4096, 64, batch=4, ta=ta, tb=tb, beta=1.0,
+                    tin="float16", epilogue=Epilogue.kBiasThenSILUWithAux)
+    assert "gemm_fast_f16" in plan.describe()
+    plan = run_case(dev, 104, 12288, 128, batch=3, ta=ta, tb=tb,
+                    epilogue=Epilogue.kBiasThenGELU)
+    assert "gemm_fast_bf16" in plan.describe()
+
+
 def test_interior_tile_kernel_not_taken(dev):
-    # rows not 16-byte aligned, K not a multiple of 64, M not of 256
-    for kw in (dict(m=2048, n=2048, k=128, pad=3), dict(m=2048, n=2048, k=96),
-               dict(m=2000, n=2048, k=128)):
+    # rows not 16-byte aligned, K not a multiple of 64
+    for kw in (dict(m=2048, n=2048, k=128, pad=3), dict(m=2048, n=2048, k=96)):
         kw = dict(kw)
         plan = run_case(dev, kw.pop("m"), kw.pop("n"), kw.pop("k"), **kw)
         assert "gemm_tile" in plan.describe()
