@@ -318,19 +318,29 @@ qk_status DispatchSplitK(const GemmArgs& g, int batch, bool ta, bool tb,
   return PostLaunch(name);
 }
 
+template <int BM, int BN, int NW, bool MC>
+qk_status DispatchF32x3M(const GemmArgs& g, int batch, bool ta, bool tb,
+                         hipStream_t stream, const char* name) {
+  dim3 grid(g.tiles_m * g.tiles_n, batch);
+  if (!ta && !tb)
+    gemm_f32x3_kernel<BM, BN, false, false, NW, MC><<<grid, NW * 64, 0, stream>>>(g);
+  else if (!ta && tb)
+    gemm_f32x3_kernel<BM, BN, false, true, NW, MC><<<grid, NW * 64, 0, stream>>>(g);
+  else if (ta && !tb)
+    gemm_f32x3_kernel<BM, BN, true, false, NW, MC><<<grid, NW * 64, 0, stream>>>(g);
+  else
+    gemm_f32x3_kernel<BM, BN, true, true, NW, MC><<<grid, NW * 64, 0, stream>>>(g);
+  return PostLaunch(name);
+}
+
+// M a multiple of BM: the kernel without row checks; otherwise the last M
+// tile is partly filled.
 template <int BM, int BN, int NW>
 qk_status DispatchF32x3(const GemmArgs& g, int batch, bool ta, bool tb,
                         hipStream_t stream, const char* name) {
-  dim3 grid(g.tiles_m * g.tiles_n, batch);
-  if (!ta && !tb)
-    gemm_f32x3_kernel<BM, BN, false, false, NW><<<grid, NW * 64, 0, stream>>>(g);
-  else if (!ta && tb)
-    gemm_f32x3_kernel<BM, BN, false, true, NW><<<grid, NW * 64, 0, stream>>>(g);
-  else if (ta && !tb)
-    gemm_f32x3_kernel<BM, BN, true, false, NW><<<grid, NW * 64, 0, stream>>>(g);
-  else
-    gemm_f32x3_kernel<BM, BN, true, true, NW><<<grid, NW * 64, 0, stream>>>(g);
-  return PostLaunch(name);
+  if (g.m % BM == 0)
+    return DispatchF32x3M<BM, BN, NW, false>(g, batch, ta, tb, stream, name);
+  return DispatchF32x3M<BM, BN, NW, true>(g, batch, ta, tb, stream, name);
 }
 
 struct TileCfg {
@@ -404,18 +414,23 @@ int ForcedHalfTile() {
 // with bm x bn tiles: f32, M, N multiples of the tile, K of 32, 16-byte
 // aligned operands and leading dimensions, and each operand of one batch
 // entry under 2^31 bytes (the extent of a buffer descriptor).
+// Any M (the last M tile may be partly filled); N and K multiples of the
+// tile; offsets, with A padded to whole tiles, under 2^31 bytes.
 bool F32x3Applies(const GemmProblem& p, int bm, int bn) {
-  if (p.a.dtype != QK_F32 || p.m % bm != 0 || p.n % bn != 0 ||
-      p.k % 32 != 0 || p.k == 0)
+  if (p.a.dtype != QK_F32 || p.m == 0 || p.n % bn != 0 || p.k % 32 != 0 ||
+      p.k == 0)
     return false;
   const bool batched = p.batch > 1;
-  auto ok = [&](const Operand& o, int64_t rows) {
+  // elems: the largest element offset a tile can address, plus one
+  auto ok = [&](const Operand& o, int64_t elems) {
     const int64_t bs = batched ? o.batch_stride : 0;
     return reinterpret_cast<uintptr_t>(o.ptr) % 16 == 0 && o.ld % 4 == 0 &&
-           bs % 4 == 0 && rows * o.ld * 4 < (int64_t{1} << 31);
+           bs % 4 == 0 && elems * 4 < (int64_t{1} << 31);
   };
-  return ok(p.a, p.a.transpose ? p.k : p.m) &&
-         ok(p.b, p.b.transpose ? p.n : p.k);
+  const int64_t mpad = (p.m + bm - 1) / bm * bm;
+  return ok(p.a, p.a.transpose ? (p.k - 1) * p.a.ld + mpad
+                               : mpad * p.a.ld) &&
+         ok(p.b, (p.b.transpose ? p.n : p.k) * p.b.ld);
 }
 
 // Whether the interior-tile kernel can run the problem with a BN-wide

@@ -72,7 +72,9 @@ __device__ __forceinline__ Split4 SplitF32x4(const u32x4& v) {
 // registers -> three bf16 tiles in LDS (TileLayout<bf16, R, BK, KCONT>).
 // Thread t loads 16-byte vectors t, t + NT, ... of the tile; vector i
 // covers source row (t / VPR) + i * RPI, elements 4 (t % VPR) .. + 3.
-template <int R, int BK, int NT, bool KCONT>
+// VC: the whole offset goes in the vector offset, which the descriptor's
+// extent checks (for tiles that run past the operand's last row).
+template <int R, int BK, int NT, bool KCONT, bool VC = false>
 struct SplitLoader {
   static constexpr int VPR = (KCONT ? BK : R) / 4;  // vectors per row
   static constexpr int RPI = NT / VPR;               // rows between vectors
@@ -93,9 +95,13 @@ struct SplitLoader {
   __device__ __forceinline__ void load(int r0, int k0) {
     const int base = KCONT ? r0 * ld + k0 : k0 * ld + r0;  // elements
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
-      v[i] = __builtin_amdgcn_raw_buffer_load_b128(
-          rsrc, voff, (base + i * RPI * ld) * 4, 0);
+    for (int i = 0; i < NV; ++i) {
+      const int so = (base + i * RPI * ld) * 4;
+      if constexpr (VC)
+        v[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff + so, 0, 0);
+      else
+        v[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, so, 0);
+    }
   }
   // Returns whether any of the thread's elements is infinite or NaN.
   __device__ __forceinline__ bool store(bf16* th, bf16* tm, bf16* tl,
@@ -129,7 +135,11 @@ __device__ __forceinline__ Frag<bf16>::type FiniteOnly(
   return __builtin_bit_cast(Frag<bf16>::type, w);
 }
 
-template <int BM, int BN, bool TA, bool TB, int NW>
+// MC: M need not be a multiple of BM: the A tile's offsets go wholly in
+// the range-checked vector offset and the epilogue skips rows past M
+// (values fetched for rows past M only reach those rows; a non-finite one
+// among them at worst costs the workgroup the masked second pass).
+template <int BM, int BN, bool TA, bool TB, int NW, bool MC = false>
 __global__ __launch_bounds__(NW * 64) void gemm_f32x3_kernel(GemmArgs g) {
   constexpr int BK = 32, NT = NW * 64, WM = NW / 2, WN = 2;
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
@@ -161,7 +171,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32x3_kernel(GemmArgs g) {
   const int m0 = tm * BM, n0 = tn * BN;
   const long long batch = blockIdx.y;
 
-  SplitLoader<BM, BK, NT, AK> la;
+  SplitLoader<BM, BK, NT, AK, MC> la;
   la.init(static_cast<const float*>(g.a) + batch * g.bsa,
           static_cast<long long>(AK ? g.m : g.k) * g.lda * 4, g.lda, tid);
   SplitLoader<BN, BK, NT, BKC> lb;
@@ -257,7 +267,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32x3_kernel(GemmArgs g) {
     __syncthreads();  // every wave has read the flag
     run(std::true_type{});
   }
-  store_direct<float, BM, BN, WM, WN>(g, acc, m0, n0, batch, lane, wm, wn);
+  store_direct<float, BM, BN, WM, WN, MC>(g, acc, m0, n0, batch, lane, wm,
+                                          wn);
 }
 
 }  // namespace

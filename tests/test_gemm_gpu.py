@@ -424,6 +424,21 @@ def test_f32_split_kernel(dev, ta, tb):
     assert "gemm_f32x3" in plan.describe()
 
 
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_f32_split_kernel_ragged_m(dev, ta, tb):
+    """M not a multiple of the split kernel's tile height: a partly
+    filled last M tile. Batched with packed batch entries, so a row written
+    past M would land in the next entry's output."""
+    plan = run_case(dev, 1000, 2048, 64, tin="float32", ta=ta, tb=tb)
+    assert "gemm_f32x3_f32_64x64" in plan.describe()
+    plan = run_case(dev, 2000, 2048, 96, tin="float32", ta=ta, tb=tb)
+    assert "gemm_f32x3_f32_128x128" in plan.describe()
+    plan = run_case(dev, 100, 128, 64, batch=3, tin="float32", ta=ta, tb=tb,
+                    beta=1.0, epilogue=Epilogue.kBiasThenSILUWithAux)
+    assert "gemm_f32x3_f32_64x64" in plan.describe()
+
+
 def test_f32_split_kernel_special_values(dev):
     """Infinities and NaNs reach the output as in an f32 product: the
     split keeps an infinite element whole in its leading part."""
