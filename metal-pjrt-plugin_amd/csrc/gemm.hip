@@ -318,29 +318,31 @@ qk_status DispatchSplitK(const GemmArgs& g, int batch, bool ta, bool tb,
   return PostLaunch(name);
 }
 
-template <int BM, int BN, int NW, bool MC>
+template <int BM, int BN, int NW, bool MC, int KS, int BK>
 qk_status DispatchF32x3M(const GemmArgs& g, int batch, bool ta, bool tb,
                          hipStream_t stream, const char* name) {
   dim3 grid(g.tiles_m * g.tiles_n, batch);
   if (!ta && !tb)
-    gemm_f32x3_kernel<BM, BN, false, false, NW, MC><<<grid, NW * 64, 0, stream>>>(g);
+    gemm_f32x3_kernel<BM, BN, false, false, NW, MC, KS, BK><<<grid, NW * 64, 0, stream>>>(g);
   else if (!ta && tb)
-    gemm_f32x3_kernel<BM, BN, false, true, NW, MC><<<grid, NW * 64, 0, stream>>>(g);
+    gemm_f32x3_kernel<BM, BN, false, true, NW, MC, KS, BK><<<grid, NW * 64, 0, stream>>>(g);
   else if (ta && !tb)
-    gemm_f32x3_kernel<BM, BN, true, false, NW, MC><<<grid, NW * 64, 0, stream>>>(g);
+    gemm_f32x3_kernel<BM, BN, true, false, NW, MC, KS, BK><<<grid, NW * 64, 0, stream>>>(g);
   else
-    gemm_f32x3_kernel<BM, BN, true, true, NW, MC><<<grid, NW * 64, 0, stream>>>(g);
+    gemm_f32x3_kernel<BM, BN, true, true, NW, MC, KS, BK><<<grid, NW * 64, 0, stream>>>(g);
   return PostLaunch(name);
 }
 
 // M a multiple of BM: the kernel without row checks; otherwise the last M
 // tile is partly filled.
-template <int BM, int BN, int NW>
+template <int BM, int BN, int NW, int KS = 1, int BK = 32>
 qk_status DispatchF32x3(const GemmArgs& g, int batch, bool ta, bool tb,
                         hipStream_t stream, const char* name) {
   if (g.m % BM == 0)
-    return DispatchF32x3M<BM, BN, NW, false>(g, batch, ta, tb, stream, name);
-  return DispatchF32x3M<BM, BN, NW, true>(g, batch, ta, tb, stream, name);
+    return DispatchF32x3M<BM, BN, NW, false, KS, BK>(g, batch, ta, tb, stream,
+                                                     name);
+  return DispatchF32x3M<BM, BN, NW, true, KS, BK>(g, batch, ta, tb, stream,
+                                                  name);
 }
 
 struct TileCfg {
@@ -632,8 +634,19 @@ qk_status LaunchGemm(const GemmProblem& p, hipStream_t stream) {
     default:
       if (c.tile == kF32x3Tile128)
         return DispatchF32x3<128, 128, 8>(g, batch, ta, tb, stream, name);
-      if (c.tile == kF32x3Tile64)
-        return DispatchF32x3<64, 64, 4>(g, batch, ta, tb, stream, name);
+      if (c.tile == kF32x3Tile64) {
+        // 64x64 tiles: 16 waves in four groups over a 64-wide K tile when
+        // K allows, else 8 in two over a 32-wide one. QK_GEMM_F32=x2
+        // forces the latter (tuning).
+        static const bool x2 = [] {
+          const char* v = std::getenv("QK_GEMM_F32");
+          return v != nullptr && std::string(v) == "x2";
+        }();
+        if (g.k % 64 == 0 && !x2)
+          return DispatchF32x3<64, 64, 16, 4, 64>(g, batch, ta, tb, stream,
+                                                  name);
+        return DispatchF32x3<64, 64, 8, 2>(g, batch, ta, tb, stream, name);
+      }
       if (c.bm == 128)
         return Dispatch<float, 128, 128, 32, 2, 2>(g, batch, ta, tb, stream, name);
       return Dispatch<float, 64, 64, 32, 2, 2>(g, batch, ta, tb, stream, name);

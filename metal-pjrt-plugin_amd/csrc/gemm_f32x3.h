@@ -139,9 +139,15 @@ __device__ __forceinline__ Frag<bf16>::type FiniteOnly(
 // the range-checked vector offset and the epilogue skips rows past M
 // (values fetched for rows past M only reach those rows; a non-finite one
 // among them at worst costs the workgroup the masked second pass).
-template <int BM, int BN, bool TA, bool TB, int NW, bool MC = false>
+// KS = 2: two groups of NW / 2 waves share the tile, group q taking the
+// 16-wide K step q of every K tile (two waves per SIMD for a tile too
+// small to keep one wave per SIMD busy); their partial tiles are summed
+// through LDS before the epilogue.
+template <int BM, int BN, bool TA, bool TB, int NW, bool MC = false,
+          int KS = 1, int BK = 32>
 __global__ __launch_bounds__(NW * 64) void gemm_f32x3_kernel(GemmArgs g) {
-  constexpr int BK = 32, NT = NW * 64, WM = NW / 2, WN = 2;
+  constexpr int NT = NW * 64, WM = NW / KS / 2, WN = 2;
+  static_assert(KS == 1 || KS == BK / 16, "one K step per wave group");
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
   static_assert(FM >= 1 && FN >= 1 && WTM % 32 == 0 && WTN % 32 == 0,
                 "wave tile");
@@ -158,8 +164,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32x3_kernel(GemmArgs g) {
     return lds + s * kStage + 3 * LA::kElems + c * LB::kElems;
   };
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ks = wave / (WM * WN), wv = wave % (WM * WN);
+  const int wm = wv / WN, wn = wv % WN;
   const int nwg = g.tiles_m * g.tiles_n;
   int bid = blockIdx.x;
   if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
@@ -207,6 +215,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32x3_kernel(GemmArgs g) {
       const int cur = kt & 1;
 #pragma unroll
       for (int s = 0; s < BK / 16; ++s) {
+        if (KS > 1 && s != ks) continue;
         F fa[3][FM], fb[3][FN];
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
@@ -266,6 +275,37 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32x3_kernel(GemmArgs g) {
   if (run(std::false_type{})) {
     __syncthreads();  // every wave has read the flag
     run(std::true_type{});
+  }
+  if constexpr (KS > 1) {
+    // Every wave is past the loop's last barrier: the stages are free.
+    // Groups 1.. write their partial tiles (lane-linear per accumulator
+    // register), group 0 adds them in group order and stores.
+    constexpr int kPart = WM * WN * FM * FN * 16 * 64;  // floats per group
+    static_assert((KS - 1) * kPart * 4 <= 2 * kStage * 2,
+                  "partial tiles fit the stages");
+    float* const red = reinterpret_cast<float*>(lds);
+    auto at = [&](int q, int i, int j, int r) {
+      return (q - 1) * kPart + (((wv * FM + i) * FN + j) * 16 + r) * 64 +
+             lane;
+    };
+    if (ks != 0) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) red[at(ks, i, j, r)] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (ks != 0) return;
+#pragma unroll
+    for (int q = 1; q < KS; ++q)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += red[at(q, i, j, r)];
   }
   store_direct<float, BM, BN, WM, WN, MC>(g, acc, m0, n0, batch, lane, wm,
                                           wn);
