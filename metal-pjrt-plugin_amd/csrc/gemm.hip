@@ -521,8 +521,14 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
       c.tile = kF32x3Tile128;
       c.bm = 128, c.bn = 128, c.bk = 32;
     } else if (!mfma_only && F32x3Applies(p, 64, 64)) {
+      // Four wave groups over 64-wide K tiles when K allows, else two over
+      // 32-wide ones; QK_GEMM_F32=x2 forces the latter (tuning).
+      static const bool x2 = [] {
+        const char* v = std::getenv("QK_GEMM_F32");
+        return v != nullptr && std::string(v) == "x2";
+      }();
       c.tile = kF32x3Tile64;
-      c.bm = 64, c.bn = 64, c.bk = 32;
+      c.bm = 64, c.bn = 64, c.bk = p.k % 64 == 0 && !x2 ? 64 : 32;
     } else if (tiles(128, 128) >= 192) {
       c.bm = 128, c.bn = 128, c.bk = 32;
     } else {
@@ -635,14 +641,9 @@ qk_status LaunchGemm(const GemmProblem& p, hipStream_t stream) {
       if (c.tile == kF32x3Tile128)
         return DispatchF32x3<128, 128, 8>(g, batch, ta, tb, stream, name);
       if (c.tile == kF32x3Tile64) {
-        // 64x64 tiles: 16 waves in four groups over a 64-wide K tile when
-        // K allows, else 8 in two over a 32-wide one. QK_GEMM_F32=x2
-        // forces the latter (tuning).
-        static const bool x2 = [] {
-          const char* v = std::getenv("QK_GEMM_F32");
-          return v != nullptr && std::string(v) == "x2";
-        }();
-        if (g.k % 64 == 0 && !x2)
+        // 64x64 tiles: 16 waves in four groups over a 64-wide K tile, or
+        // 8 in two over a 32-wide one (ChooseGemmKernel's bk).
+        if (c.bk == 64)
           return DispatchF32x3<64, 64, 16, 4, 64>(g, batch, ta, tb, stream,
                                                   name);
         return DispatchF32x3<64, 64, 8, 2>(g, batch, ta, tb, stream, name);
