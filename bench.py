@@ -10,7 +10,8 @@ weights another launch left in the 256 MB Infinity Cache.
 
 Also reported (`secondary`): bf16 GEMM + bias + SiLU TFLOP/s at the C3
 shapes (the metric's second half), int4 M = 16 / 512, int8 affine GEMV,
-RMSNorm and softmax [4096, 4096] HBM GB/s; each against its roofline.
+RMSNorm, softmax and LayerNorm [4096, 4096] HBM GB/s; each against its
+roofline.
 
 Timing: the W warm-up steps and the K timed steps are each captured into a
 HIP graph (the launches only: outputs are preallocated, nothing is
@@ -212,19 +213,26 @@ def secondary(torch, qkern, dev, gen):
                     "frac": round(gbs / HBM_PEAK_GBS, 4)})
     del sets8
     # rownorm [4096, 4096]
+    # (LayerNorm with gain and offset, eps 1e-5, beside the configured
+    # RMSNorm and softmax)
     for name, kind, dt, esz in [("rmsnorm bf16", 0, torch.bfloat16, 2),
                                 ("rmsnorm f32", 0, torch.float32, 4),
-                                ("softmax f32", 2, torch.float32, 4)]:
+                                ("softmax f32", 2, torch.float32, 4),
+                                ("layernorm bf16", 1, torch.bfloat16, 2)]:
         xs = [torch.randn(4096, 4096, device=dev, generator=gen).to(dt)
               for _ in range(8)]
         ys = [torch.empty_like(xs[0]) for _ in range(2)]
         g = (1 + 0.1 * torch.randn(4096, device=dev, generator=gen))
-        gain = g if kind == 0 else None
-        fn = lambda i: qkern.rownorm(xs[i % 8], kind, eps=1e-6, gain=gain,
-                                     out=ys[i % 2])
+        bt = 0.1 * torch.randn(4096, device=dev, generator=gen)
+        gain = g if kind != 2 else None
+        beta = bt if kind == 1 else None
+        eps = 1e-5 if kind == 1 else 1e-6
+        fn = lambda i: qkern.rownorm(xs[i % 8], kind, eps=eps, gain=gain,
+                                     beta=beta, out=ys[i % 2])
         fn(0)
         ms = timed_launches(torch, fn, 32)
-        nbytes = 2 * 4096 * 4096 * esz + (4096 * 4 if kind == 0 else 0)
+        nbytes = (2 * 4096 * 4096 * esz + (4096 * 4 if kind != 2 else 0) +
+                  (4096 * 4 if kind == 1 else 0))
         gbs = nbytes / (ms * 1e-3) / 1e9
         out.append({"name": f"{name} 4096x4096", "value": round(gbs, 1),
                     "unit": "GB/s", "ms": round(ms, 4),

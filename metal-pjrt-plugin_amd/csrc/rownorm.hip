@@ -521,6 +521,11 @@ bool LaunchStream(const RnArgs& a, hipStream_t st) {
   // (two 16-vector buffers per wave measured slower than the one-shot
   // kernel).
   if (a.n <= 64 * V * 4) return go(rownorm_stream_kernel<T, KIND, V, 4>);
+  // LayerNorm of 16-bit rows (gain and offset held as f32): 8 vectors per
+  // lane take 256 VGPRs, one wave per SIMD; two waves of 4 keep two per
+  // SIMD ([4096, 4096] bf16: 16.7 -> 14.5 us).
+  if (KIND == QK_ROWNORM_LAYER && V == 8 && a.n <= 64 * V * 8)
+    return go(rownorm_stream_kernel<T, KIND, V, 4, 2>, 2);
   if (a.n <= 64 * V * 8) return go(rownorm_stream_kernel<T, KIND, V, 8>);
   if (a.n <= 64 * V * 16)
     return go(rownorm_stream_kernel<T, KIND, V, 8, 2>, 2);

@@ -91,13 +91,16 @@ def test_rownorm_shapes(dev, kind, dtype):
 def test_rownorm_many_rows(dev, kind, dtype):
     """Enough rows for the persistent streaming kernel (several rows per
     wave, a ragged last round), for each register size class (rows of up
-    to 16 vectors per lane shared by two waves), with gains and offsets of
+    to 16 vectors per lane shared by two waves; 16-bit layer norm rows of
+    up to 8 vectors per lane on two waves of 4), with gains and offsets of
     the row type and of f32."""
     rng = np.random.default_rng(10 + int(kind))
     cases = [(4099, 1000, "float32"), (4101, 4096, dtype),
              (4097, 8192 if dtype != "float32" else 4104, "float32"),
              # two waves per row with a partly filled second half
-             (4103, 3000 if dtype == "float32" else 6000, dtype)]
+             (4103, 3000 if dtype == "float32" else 6000, dtype),
+             # 16-bit layer norm: two waves of four vectors per lane
+             (4099, 2500, dtype)]
     for rows, n, pdtype in cases:
         x = rng.standard_normal((rows, n)) * (2.0 if kind == 2 else 1.0) + 0.3
         gain = beta = None
