@@ -20,8 +20,8 @@
 //  - Workgroup ids are remapped so that consecutive tiles share an XCD
 //    (the hardware deals workgroups round-robin over the 8 XCDs, each with
 //    its own L2) and tiles are visited in groups of GROUP_M tile rows.
-//  - Problems that are whole multiples of 256 x BN x 64 with 16-byte
-//    aligned operands take gemm_dma_kernel (gemm_dma.h): operand tiles go
+//  - Problems whose N and K are multiples of BN x 64 (any M) with
+//    16-byte aligned operands take gemm_dma_kernel (gemm_dma.h): operand tiles go
 //    from global memory straight into XOR-swizzled LDS stages, and the
 //    epilogue is applied from the accumulators without LDS staging.
 
@@ -413,11 +413,10 @@ int ForcedHalfTile() {
 }
 
 // Whether the split-bf16 f32 kernel (gemm_f32x3.h) can run the problem
-// with bm x bn tiles: f32, M, N multiples of the tile, K of 32, 16-byte
-// aligned operands and leading dimensions, and each operand of one batch
-// entry under 2^31 bytes (the extent of a buffer descriptor).
-// Any M (the last M tile may be partly filled); N and K multiples of the
-// tile; offsets, with A padded to whole tiles, under 2^31 bytes.
+// with bm x bn tiles: f32, any M (the last M tile may be partly filled),
+// N a multiple of the tile, K of 32, 16-byte aligned operands and leading
+// dimensions, and each operand of one batch entry, with A padded to whole
+// tiles, under 2^31 bytes (the extent of a buffer descriptor).
 bool F32x3Applies(const GemmProblem& p, int bm, int bn) {
   if (p.a.dtype != QK_F32 || p.m == 0 || p.n % bn != 0 || p.k % 32 != 0 ||
       p.k == 0)

@@ -461,9 +461,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs g) {
 // Interior-tile f16/bf16 kernel with a register-staged B source (used by
 // the quantized matmul, whose B tile is dequantized on its way into LDS;
 // dense operands take the LDS-DMA kernel of gemm_dma.h) for problems whose
-// M, N and K are multiples of the tile (BM = 256, BN = 256 or 128,
-// BK = 64) and whose operands allow 16-byte loads: no bounds checks in the
-// K loop.
+// N and K are multiples of the tile (BM = 256 or 128, BN = 256 or 128,
+// BK = 64; M too unless MC) and whose operands allow 16-byte loads: no
+// bounds checks in the K loop.
 //
 //  - Four waves (2 x 2), each owning a 128 x BN/2 block of D: 16 (or 8)
 //    32x32 accumulators, so one wave per SIMD keeps every MFMA pipe fed.

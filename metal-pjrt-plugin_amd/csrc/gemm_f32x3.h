@@ -17,8 +17,8 @@
 // with, in the cross terms, h's infinities and NaNs replaced by zero (the
 // common, all-finite case pays only the loaders' check).
 //
-// Interior tiles only (M, N multiples of the tile, K of 32, 16-byte
-// aligned operands): the operand tiles are read with buffer loads into
+// Interior tiles (N a multiple of the tile, K of 32, any M: the last M
+// tile may be partly filled; 16-byte aligned operands): the operand tiles are read with buffer loads into
 // registers, split, and written as three bf16 tiles per operand into LDS
 // in the layouts of the bf16 kernels (gemm_common.h TileLayout), so the
 // fragment reads and MFMAs are those of the bf16 interior-tile kernel.
