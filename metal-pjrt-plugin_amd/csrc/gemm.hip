@@ -637,8 +637,8 @@ qk_status LaunchGemm(const GemmProblem& p, hipStream_t stream) {
     case QK_F16:
       return DispatchHalf<f16>(c.tile, g, batch, ta, tb, stream, name);
     default:
-      if (c.tile == kF32x3Tile128)
-        return DispatchF32x3<128, 128, 8>(g, batch, ta, tb, stream, name);
+      if (c.tile == kF32x3Tile128)  // 16 waves in two K-step groups
+        return DispatchF32x3<128, 128, 16, 2>(g, batch, ta, tb, stream, name);
       if (c.tile == kF32x3Tile64) {
         // 64x64 tiles: 16 waves in four groups over a 64-wide K tile, or
         // 8 in two over a 32-wide one (ChooseGemmKernel's bk).
