@@ -244,10 +244,15 @@ qk_status qk_rownorm(void* stream, const qk_buffer* x, const qk_buffer* gain,
 const char* qk_last_error_message(void);
 
 /* QK_OK, or the sticky device error (its message in
- * qk_last_error_message()). */
+ * qk_last_error_message()). Also reads the device status word of every
+ * device used so far (a blocking read; synchronize the streams first): a
+ * kernel whose bounded wait between producer and consumer waves gave up
+ * (after QK_SPIN_LIMIT polls, default 2^20) stores NaN outputs and sets
+ * that word, and it becomes the sticky QK_INTERNAL error here. */
 qk_status qk_device_error(void);
 
-/* Clears the sticky device error and re-reads QK_FAIL_LAUNCH (tests). */
+/* Clears the sticky device error and the device status words, and
+ * re-reads QK_FAIL_LAUNCH and QK_SPIN_LIMIT (tests). */
 void qk_reset_device_error(void);
 
 /* Library version string. */

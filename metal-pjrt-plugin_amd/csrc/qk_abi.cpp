@@ -37,7 +37,24 @@ std::atomic<int64_t> g_launches{0};
 std::atomic<int64_t> g_fail_at{-1};  // -1: not read yet; 0: disabled
 std::once_flag g_env_once;
 
+// QK_SPIN_LIMIT: polls before a bounded flag wait gives up (tests force a
+// timeout with 0; every wait still ends).
+std::atomic<int> g_spin_limit{1 << 20};
+
+void ReadSpinEnv() {
+  const char* v = std::getenv("QK_SPIN_LIMIT");
+  int n = 1 << 20;
+  if (v != nullptr && *v != '\0') {
+    char* end = nullptr;
+    long long parsed = std::strtoll(v, &end, 10);
+    if (end != v && *end == '\0' && parsed >= 0 && parsed <= (1 << 24))
+      n = static_cast<int>(parsed);
+  }
+  g_spin_limit.store(n);
+}
+
 void ReadFailEnv() {
+  ReadSpinEnv();
   const char* v = std::getenv("QK_FAIL_LAUNCH");
   int64_t n = 0;
   if (v != nullptr && *v != '\0') {
@@ -57,6 +74,13 @@ void SetSticky(qk_status s, const std::string& msg) {
 }
 
 }  // namespace
+
+int SpinLimit() {
+  std::call_once(g_env_once, [] {
+    if (g_fail_at.load() < 0) ReadFailEnv();
+  });
+  return g_spin_limit.load();
+}
 
 qk_status Fail(qk_status s, const std::string& msg) {
   g_last_error = msg;
@@ -339,14 +363,28 @@ extern "C" qk_status qk_gemm_plan_create(const qk_gemm_config* cfg,
                       l->leading_dim_stride, kMaxLd);
       }
     }
-  } else if (!epi.trivial() &&
-             (m > UINT32_MAX || n > UINT32_MAX || batch > UINT32_MAX)) {
-    return Fail(QK_UNIMPLEMENTED,
-                "qkern: f32 matmul with a fused bias or activation on a " +
-                    std::to_string(batch) + "x" + std::to_string(m) + "x" +
-                    std::to_string(n) +
-                    " output: each dimension must be below 2^32. Split the "
-                    "matmul");
+  } else {
+    // The f32 kernels take every dimension and leading dimension as a
+    // 32-bit int (row offsets are formed in 64 bits): refuse what does not
+    // fit instead of truncating it, as the reference refuses what its
+    // kernels cannot index (blas_lt_support.cc:166-199).
+    auto refuse = [&](const char* what, int64_t value) {
+      return Fail(QK_UNIMPLEMENTED,
+                  std::string("qkern: f32 matmul too large: the f32 matmul "
+                              "kernels take 32-bit sizes, and its ") +
+                      what + " " + std::to_string(value) + " exceeds " +
+                      std::to_string(kMaxInt) + ". Split the matmul");
+    };
+    if (batch > kMaxInt) return refuse("batch count", batch);
+    for (int64_t dim : {m, n, k}) {
+      if (dim > kMaxInt) return refuse("dimension", dim);
+    }
+    for (const qk_matrix_layout* l : {&lhs, &rhs, &out}) {
+      if (l->leading_dim_stride > kMaxInt) {
+        return refuse("leading dimension (elements between rows)",
+                      l->leading_dim_stride);
+      }
+    }
   }
 
   // The plan (reference GetMatmulPlan, metal_blas.cc:245-287): a row-major
@@ -392,7 +430,8 @@ extern "C" const char* qk_gemm_plan_describe(const qk_gemm_plan* plan) {
       "m=%" PRId64 " n=%" PRId64 " k=%" PRId64 " batch=%" PRId64
       " alpha=%g beta=%g a={%s ld=%" PRId64 " bs=%" PRId64 "%s} b={%s ld=%" PRId64
       " bs=%" PRId64 "%s} d={%s ld=%" PRId64 " bs=%" PRId64
-      "} swap=%d bias=%d aux=%d act=%d kernel=%s",
+      "} swap=%d bias=%d aux=%d act=%d kernel=%s (if 16-byte aligned; "
+      "chosen again from the buffers at execute)",
       p.m, p.n, p.k, p.batch, p.alpha, plan->beta, qk::DTypeName(p.a.dtype),
       p.a.ld, p.a.batch_stride, p.a.transpose ? " T" : "",
       qk::DTypeName(p.b.dtype), p.b.ld, p.b.batch_stride,
@@ -507,10 +546,34 @@ extern "C" qk_status qk_gemm_execute(const qk_gemm_plan* plan, void* stream,
 
 namespace {
 
-int64_t NumElements(const qk_buffer& b) {
+// Buffers hold at most 2^56 elements: element counts, byte counts and the
+// products of two checked sizes below stay far from int64 overflow.
+constexpr int64_t kMaxElements = int64_t{1} << 56;
+
+// Element count of b, or -1 when it overflows kMaxElements. Dimensions are
+// non-negative (CheckBuffer); a zero dimension gives 0 whatever the others.
+int64_t CountElements(const qk_buffer& b) {
   int64_t n = 1;
-  for (int i = 0; i < b.rank; ++i) n *= b.dims[i];
-  return n;
+  bool over = false;
+  for (int i = 0; i < b.rank; ++i) {
+    if (b.dims[i] == 0) return 0;
+    if (__builtin_mul_overflow(n, b.dims[i], &n) || n > kMaxElements) {
+      over = true;
+      n = 1;
+    }
+  }
+  return over ? -1 : n;
+}
+
+// Element count of a buffer CheckBuffer accepted (never overflows).
+int64_t NumElements(const qk_buffer& b) { return CountElements(b); }
+
+// a * b for sizes from accepted buffers; -1 when the product overflows
+// kMaxElements (such a product never matches an accepted element count).
+int64_t MulSizes(int64_t a, int64_t b) {
+  int64_t r = 0;
+  if (__builtin_mul_overflow(a, b, &r) || r > kMaxElements) return -1;
+  return r;
 }
 
 std::string BufferString(const qk_buffer& b) {
@@ -539,6 +602,10 @@ qk_status CheckBuffer(const qk_buffer* b, const char* name, bool allow_null) {
       return Fail(QK_INVALID_ARGUMENT, std::string("qkern: ") + name +
                                            " has a negative dimension");
     }
+  }
+  if (CountElements(*b) < 0) {
+    return Fail(QK_INVALID_ARGUMENT,
+                std::string("qkern: ") + name + " has more than 2^56 elements");
   }
   if (b->data == nullptr && NumElements(*b) > 0) {
     return Fail(QK_INVALID_ARGUMENT,
@@ -605,7 +672,8 @@ qk_status CheckQuant(const qk_buffer* codes, const qk_buffer* scales,
                     " is not a multiple of the group size " +
                     std::to_string(g));
   }
-  if (codes->rank < 2 || NumElements(*codes) * codes_per_elem != n * k) {
+  if (codes->rank < 2 ||
+      NumElements(*codes) * codes_per_elem != MulSizes(n, k)) {
     return Fail(QK_INVALID_ARGUMENT,
                 "qkern: codes " + BufferString(*codes) + " do not hold " +
                     std::to_string(n) + "x" + std::to_string(k) +
@@ -620,7 +688,7 @@ qk_status CheckQuant(const qk_buffer* codes, const qk_buffer* scales,
   }
   auto check_sb = [&](const qk_buffer* b, const char* name) -> qk_status {
     if (!IsFloat(b->dtype) || b->dims[0] != n ||
-        NumElements(*b) != n * (k / g)) {
+        NumElements(*b) != MulSizes(n, k / g)) {
       return Fail(QK_INVALID_ARGUMENT,
                   std::string("qkern: ") + name + " must be float [N, K/g] = [" +
                       std::to_string(n) + ", " + std::to_string(k / g) +
@@ -672,7 +740,7 @@ extern "C" qk_status qk_qmatvec(void* stream, const qk_buffer* x,
   }
   const int64_t m = k == 0 ? 0 : NumElements(*x) / k;
   if (y->dtype != x->dtype || y->dims[y->rank - 1] != q.n ||
-      NumElements(*y) != m * q.n) {
+      NumElements(*y) != MulSizes(m, q.n)) {
     return Fail(QK_INVALID_ARGUMENT,
                 "qkern: qmatvec output must be " +
                     std::string(qk::DTypeName(x->dtype)) + " [..., " +
@@ -800,6 +868,15 @@ extern "C" const char* qk_last_error_message(void) {
 }
 
 extern "C" qk_status qk_device_error(void) {
+  // Kernels that gave up a bounded wait (their outputs are NaN) set a bit
+  // in the device status word; it becomes the sticky error here.
+  if (qk::g_sticky_status.load() == QK_OK &&
+      (qk::ReadDeviceStatusWords(false) & 1u) != 0u) {
+    qk::SetSticky(QK_INTERNAL,
+                  "a quantized matmul kernel gave up waiting between its "
+                  "producer and consumer waves (its outputs were set to "
+                  "NaN)");
+  }
   const int s = qk::g_sticky_status.load();
   if (s != QK_OK) {
     std::lock_guard<std::mutex> lock(qk::g_sticky_mu);
@@ -814,6 +891,7 @@ extern "C" void qk_reset_device_error(void) {
     qk::g_sticky_message.clear();
     qk::g_sticky_status.store(QK_OK);
   }
+  (void)qk::ReadDeviceStatusWords(true);
   qk::g_launches.store(0);
   qk::ReadFailEnv();
   qk::g_last_error.clear();

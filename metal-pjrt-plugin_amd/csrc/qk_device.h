@@ -237,4 +237,32 @@ __device__ __forceinline__ void LdsStoreVolatile(uint32_t* p, uint32_t v) {
   *(P)p = v;
 }
 
+// Bit set in the device status word when a wait between the producer and
+// consumer waves of a workgroup gave up.
+constexpr uint32_t kStatusSpinTimeout = 1u;
+
+// A bounded wait for an LDS flag written by another wave of the workgroup:
+// polls until *f == want, at most `limit` polls. A wave that gives up sets
+// the workgroup's *late word and goes on, so the kernel still ends; the
+// workgroup then stores NaN outputs and reports the timeout through
+// ReportLate.
+__device__ __forceinline__ void SpinUntil(const uint32_t* f, uint32_t want,
+                                          int limit, uint32_t* late) {
+  for (int it = 0; it < limit; ++it) {
+    if (__builtin_amdgcn_readfirstlane(LdsLoadVolatile(f)) == want) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  LdsStoreVolatile(late, 1u);
+}
+
+// Called by one lane once the workgroup's waits are over: a workgroup that
+// gave up a wait ORs kStatusSpinTimeout into the device status word (a
+// global atomic, read back by qk_device_error()).
+__device__ __forceinline__ void ReportLate(const uint32_t* late,
+                                           uint32_t* status) {
+  if (LdsLoadVolatile(late) != 0u)
+    __hip_atomic_fetch_or(status, kStatusSpinTimeout, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace qk

@@ -28,6 +28,18 @@ qk_status PostLaunch(const char* kernel);
 
 int DTypeSize(int dtype);
 
+// Polls a bounded flag wait makes before it gives up (QK_SPIN_LIMIT in the
+// environment, read with QK_FAIL_LAUNCH; default 2^20, ~70 ms).
+int SpinLimit();
+
+// Address of the device status word on the current device (qmatvec.hip),
+// or null when it cannot be resolved. Kernels OR kStatus* bits into it.
+uint32_t* DeviceStatusWord();
+
+// OR of the status words of every device a kernel has been given one for
+// (a blocking read: finished kernels only); clears them when `clear`.
+uint32_t ReadDeviceStatusWords(bool clear);
+
 // Compute units of the current device (cached per device).
 int DeviceComputeUnits();
 
@@ -93,8 +105,8 @@ struct QuantProblem {
 
 qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream);
 
-// Quantized matmul for 2..64 rows of x (qskinny.hip): int4 u32x8, bf16,
-// group 64.
+// Quantized matmul for 5..32 rows of x (qskinny.hip): int4 u32x8 or
+// int8, bf16, group 64.
 bool QSkinnyApplies(const QuantProblem& p);
 qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream);
 

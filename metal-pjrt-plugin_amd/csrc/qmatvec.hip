@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
+#include <mutex>
 
 #include <algorithm>
 #include <cstdint>
@@ -34,6 +35,60 @@
 #include "qk_internal.h"
 
 namespace qk {
+
+// The device status word: one per device (each GPU holds its own copy of
+// this variable), set by kernels whose bounded waits gave up.
+static __device__ uint32_t g_device_status;
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_status_mu;
+uint32_t* g_status_ptr[kMaxDevices] = {};
+}  // namespace
+
+uint32_t* DeviceStatusWord() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_status_mu);
+  if (g_status_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_device_status)) !=
+            hipSuccess ||
+        ptr == nullptr) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    g_status_ptr[dev] = static_cast<uint32_t*>(ptr);
+  }
+  return g_status_ptr[dev];
+}
+
+uint32_t ReadDeviceStatusWords(bool clear) {
+  std::lock_guard<std::mutex> lock(g_status_mu);
+  uint32_t bits = 0;
+  int cur = -1;
+  for (int dev = 0; dev < kMaxDevices; ++dev) {
+    if (g_status_ptr[dev] == nullptr) continue;
+    if (cur < 0 && hipGetDevice(&cur) != hipSuccess) cur = 0;
+    if (hipSetDevice(dev) != hipSuccess) continue;
+    uint32_t v = 0;
+    if (hipMemcpy(&v, g_status_ptr[dev], sizeof(v), hipMemcpyDeviceToHost) ==
+        hipSuccess)
+      bits |= v;
+    if (clear) {
+      const uint32_t zero = 0;
+      (void)hipMemcpy(g_status_ptr[dev], &zero, sizeof(zero),
+                      hipMemcpyHostToDevice);
+    }
+  }
+  if (cur >= 0) (void)hipSetDevice(cur);
+  (void)hipGetLastError();
+  return bits;
+}
+
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -1325,8 +1380,8 @@ qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream) {
   const int m = static_cast<int>(p.m);
   // Beyond four rows the reference's linear() (ROWS_MAX = 4,
   // examples/llm/qwen3.py:215-230) dequantizes to x's type and multiplies.
-  // Up to 64 rows of int4 (32 of int8) codes stream through MFMA with the
-  // codes kept factored per group (qskinny.hip); up to 128 rows dequantize
+  // Up to 32 rows (int4 and int8) stream through MFMA with the codes kept
+  // factored per group (qskinny.hip); up to 128 rows dequantize
   // in registers with K split over the waves of a workgroup (qmid.hip);
   // otherwise dequantize and multiply in one fused MFMA GEMM (qgemm.hip).
   if (m > 4 && QSkinnyApplies(p)) return LaunchQSkinny(p, stream);

@@ -61,6 +61,8 @@ struct MdArgs {
   int groups;  // k / 64
   int has_bias;
   int gpw;     // groups per wave
+  uint32_t* status;  // device status word (producer / consumer kernel)
+  int spin_limit;    // polls before a flag wait gives up
 };
 
 constexpr int kNonTemporal = 2;
@@ -318,7 +320,7 @@ qmm_wsmid_kernel(MdArgs a) {
   static_assert(kFly >= 1 && S >= NP * kFly + 1, "ring depth");
   static_assert(S * kSlot >= NC * TM * TS * 4, "partial tiles fit");
   __shared__ __attribute__((aligned(16))) unsigned char ring[S * kSlot];
-  __shared__ uint32_t flags[2 * S];  // ready[S], freed[S]
+  __shared__ uint32_t flags[2 * S + 1];  // ready[S], freed[S], late
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -327,15 +329,14 @@ qmm_wsmid_kernel(MdArgs a) {
   const int G = a.groups;
   uint32_t* const ready = flags;
   uint32_t* const freed = flags + S;
-  if (threadIdx.x < 2 * S) LdsStoreVolatile(flags + threadIdx.x, 0);
+  uint32_t* const late = flags + 2 * S;
+  if (threadIdx.x < 2 * S + 1) LdsStoreVolatile(flags + threadIdx.x, 0);
   __syncthreads();
-  // A spin of at most 2^20 polls (~70 ms): a wave that waits longer gives
-  // up and goes on (wrong results, but the kernel ends).
-  auto spin_until = [](const uint32_t* f, uint32_t want) {
-    for (int it = 0; it < (1 << 20); ++it) {
-      if (__builtin_amdgcn_readfirstlane(LdsLoadVolatile(f)) == want) return;
-      __builtin_amdgcn_s_sleep(1);
-    }
+  // Bounded waits (a.spin_limit polls, ~70 ms by default): a wave that
+  // gives up marks the workgroup late and goes on, so the kernel ends; a
+  // late workgroup stores NaN and reports the timeout.
+  auto spin_until = [&](const uint32_t* f, uint32_t want) {
+    SpinUntil(f, want, a.spin_limit, late);
   };
 
   f32x4 acc[MB][NB];
@@ -475,13 +476,16 @@ qmm_wsmid_kernel(MdArgs a) {
   }
   __syncthreads();
   bf16* Y = static_cast<bf16*>(a.y);
+  const bool bad = LdsLoadVolatile(late) != 0u;  // a wait gave up
+  if (threadIdx.x == 0) ReportLate(late, a.status);
   for (int e = threadIdx.x; e < TM * NR; e += (NC + NP) * 64) {
     const int r = e / NR, c = e % NR;
     if (r >= a.m || n0 + c >= a.n) continue;
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < NC; ++w) v += part[(w * TM + r) * TS + c];
-    Y[static_cast<long long>(r) * a.n + n0 + c] = from_f32<bf16>(v);
+    Y[static_cast<long long>(r) * a.n + n0 + c] =
+        from_f32<bf16>(bad ? __builtin_nanf("") : v);
   }
 }
 
@@ -516,6 +520,11 @@ qk_status LaunchQMid(const QuantProblem& p, hipStream_t stream) {
   a.k = static_cast<int>(p.k);
   a.groups = a.k / 64;
   a.has_bias = p.has_bias ? 1 : 0;
+  a.status = DeviceStatusWord();
+  a.spin_limit = SpinLimit();
+  if (a.status == nullptr) {
+    return Fail(QK_INTERNAL, "qkern: the device status word is unavailable");
+  }
   // Four K slices, one wave each (one per SIMD), one workgroup per CU.
   constexpr int KW = 4;
   a.gpw = a.groups / KW;  // k % 256 == 0

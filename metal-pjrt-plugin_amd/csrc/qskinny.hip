@@ -67,6 +67,8 @@ struct SkArgs {
   int groups;  // k / 64
   int has_bias;
   int chunks;  // 256-K sub-chunks per wave
+  uint32_t* status;  // device status word (producer / consumer kernels)
+  int spin_limit;    // polls before a flag wait gives up
 };
 
 constexpr int kNonTemporal = 2;
@@ -433,7 +435,7 @@ qmm_ws_kernel(SkArgs a) {
   static_assert(S >= NP * kFly + 1, "ring depth");
   static_assert(S * kSlot >= NC * TM * TS * 4, "partial tiles fit");
   __shared__ __attribute__((aligned(16))) unsigned char ring[S * kSlot];
-  __shared__ uint32_t flags[2 * S];  // ready[S], freed[S]
+  __shared__ uint32_t flags[2 * S + 1];  // ready[S], freed[S], late
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -442,16 +444,15 @@ qmm_ws_kernel(SkArgs a) {
   const int items = G / 4;
   uint32_t* const ready = flags;
   uint32_t* const freed = flags + S;
-  if (threadIdx.x < 2 * S) LdsStoreVolatile(flags + threadIdx.x, 0);
+  uint32_t* const late = flags + 2 * S;
+  if (threadIdx.x < 2 * S + 1) LdsStoreVolatile(flags + threadIdx.x, 0);
   __syncthreads();
 
-  // A spin of at most 2^20 polls (~70 ms): a wave that waits longer gives
-  // up and goes on (wrong results, but the kernel ends).
-  auto spin_until = [](const uint32_t* f, uint32_t want) {
-    for (int it = 0; it < (1 << 20); ++it) {
-      if (__builtin_amdgcn_readfirstlane(LdsLoadVolatile(f)) == want) return;
-      __builtin_amdgcn_s_sleep(1);
-    }
+  // Bounded waits (a.spin_limit polls, ~70 ms by default): a wave that
+  // gives up marks the workgroup late and goes on, so the kernel ends; a
+  // late workgroup stores NaN and reports the timeout.
+  auto spin_until = [&](const uint32_t* f, uint32_t want) {
+    SpinUntil(f, want, a.spin_limit, late);
   };
 
   f32x4 acc[MB][NB];
@@ -665,13 +666,16 @@ qmm_ws_kernel(SkArgs a) {
   }
   __syncthreads();
   bf16* Y = static_cast<bf16*>(a.y);
+  const bool bad = LdsLoadVolatile(late) != 0u;  // a wait gave up
+  if (threadIdx.x == 0) ReportLate(late, a.status);
   for (int e = threadIdx.x; e < TM * NR; e += (NC + NP) * 64) {
     const int r = e / NR, c = e % NR;
     if (r >= a.m || n0 + c >= a.n) continue;
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < NC; ++w) v += part[(w * TM + r) * TS + c];
-    Y[static_cast<long long>(r) * a.n + n0 + c] = from_f32<bf16>(v);
+    Y[static_cast<long long>(r) * a.n + n0 + c] =
+        from_f32<bf16>(bad ? __builtin_nanf("") : v);
   }
 }
 
@@ -724,7 +728,8 @@ qmm_wsp_kernel(SkArgs a) {
   static_assert(S >= NP * kFly + 1, "ring depth");
   __shared__ __attribute__((aligned(16))) unsigned char ring[S * kSlot];
   __shared__ __attribute__((aligned(16))) float part[2][kPart];
-  __shared__ uint32_t flags[2 * S + 4];  // ready[S], freed[S], cnt[2], done[2]
+  // ready[S], freed[S], cnt[2], done[2], late
+  __shared__ uint32_t flags[2 * S + 5];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -738,19 +743,18 @@ qmm_wsp_kernel(SkArgs a) {
   uint32_t* const freed = flags + S;
   uint32_t* const cnt = flags + 2 * S;
   uint32_t* const done = flags + 2 * S + 2;
-  if (threadIdx.x < 2 * S + 4) LdsStoreVolatile(flags + threadIdx.x, 0);
+  uint32_t* const late = flags + 2 * S + 4;
+  if (threadIdx.x < 2 * S + 5) LdsStoreVolatile(flags + threadIdx.x, 0);
   __syncthreads();
   auto block_n0 = [&](int i) {
     return (static_cast<int>(blockIdx.x) + i * static_cast<int>(gridDim.x)) *
            NR;
   };
-  // A spin of at most 2^20 polls (~70 ms): a wave that waits longer gives
-  // up and goes on (wrong results, but the kernel ends).
-  auto spin_until = [](const uint32_t* f, uint32_t want) {
-    for (int it = 0; it < (1 << 20); ++it) {
-      if (__builtin_amdgcn_readfirstlane(LdsLoadVolatile(f)) == want) return;
-      __builtin_amdgcn_s_sleep(1);
-    }
+  // Bounded waits (a.spin_limit polls, ~70 ms by default): a wave that
+  // gives up marks the workgroup late and goes on, so the kernel ends; a
+  // late workgroup stores NaN and reports the timeout.
+  auto spin_until = [&](const uint32_t* f, uint32_t want) {
+    SpinUntil(f, want, a.spin_limit, late);
   };
 
   if (wave >= NC) {
@@ -823,6 +827,7 @@ qmm_wsp_kernel(SkArgs a) {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     for (; published < issued; ++published) publish(p + NP * published);
+    if (lane == 0) ReportLate(late, a.status);
     return;
   }
 
@@ -925,21 +930,37 @@ qmm_wsp_kernel(SkArgs a) {
     old = __builtin_amdgcn_readfirstlane(old);
     asm volatile("" ::: "memory");  // the partial tiles' reads stay below
     if (old == NC - 1) {
-      // four consecutive columns per lane and step
+      // four consecutive columns per lane and step; NaN once a wait of
+      // this workgroup gave up
       const int n0 = block_n0(i);
       bf16* Y = static_cast<bf16*>(a.y);
-      for (int e = lane; e < 4 * NR; e += 64) {
+      constexpr int kIt = 4 * NR / 64;
+      static_assert(kIt * 64 == 4 * NR, "whole steps");
+      f32x4 v[kIt];
+#pragma unroll
+      for (int it = 0; it < kIt; ++it) {
+        const int e = lane + 64 * it;
         const int r = e / (NR / 4), c = 4 * (e % (NR / 4));
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        v[it] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < NC; ++w)
-          v += *reinterpret_cast<const f32x4*>(pb + (w * 16 + r) * TS + c);
+          v[it] += *reinterpret_cast<const f32x4*>(pb + (w * 16 + r) * TS + c);
+      }
+      // late is read after every partial has been read: a wave that gave
+      // up its wait for this buffer set it before writing into the buffer,
+      // so a sum that saw such a write also sees late.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const bool bad = LdsLoadVolatile(late) != 0u;
+#pragma unroll
+      for (int it = 0; it < kIt; ++it) {
+        const int e = lane + 64 * it;
+        const int r = e / (NR / 4), c = 4 * (e % (NR / 4));
         if (r < a.m) {
 #pragma unroll
           for (int q = 0; q < 4; ++q)
             if (n0 + c + q < a.n)
               Y[static_cast<long long>(r) * a.n + n0 + c + q] =
-                  from_f32<bf16>(v[q]);
+                  from_f32<bf16>(bad ? __builtin_nanf("") : v[it][q]);
         }
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -949,6 +970,24 @@ qmm_wsp_kernel(SkArgs a) {
       }
     }
   }
+  // Once its own work is over, a consumer that finds the workgroup late
+  // overwrites a share of all the workgroup's outputs with NaN: a wait that
+  // gave up can also leave a row block's partial count wrong, so that the
+  // block is never stored. A store that lands after this one read late as
+  // 0 after reading its partials, so its sum was complete and correct.
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if (LdsLoadVolatile(late) != 0u) {
+    bf16* Y = static_cast<bf16*>(a.y);
+    const int per_block = a.m * NR;
+    for (int e = wave * 64 + lane; e < rbs * per_block; e += NC * 64) {
+      const int i = e / per_block, rem = e % per_block;
+      const int r = rem / NR, c = block_n0(i) + rem % NR;
+      if (c < a.n)
+        Y[static_cast<long long>(r) * a.n + c] =
+            from_f32<bf16>(__builtin_nanf(""));
+    }
+  }
+  if (lane == 0) ReportLate(late, a.status);
 }
 
 }  // namespace
@@ -985,6 +1024,11 @@ qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream) {
   a.k = static_cast<int>(p.k);
   a.groups = a.k / 64;
   a.has_bias = p.has_bias ? 1 : 0;
+  a.status = DeviceStatusWord();
+  a.spin_limit = SpinLimit();
+  if (a.status == nullptr) {
+    return Fail(QK_INTERNAL, "qkern: the device status word is unavailable");
+  }
   const int cus = DeviceComputeUnits();
   const int mb = (a.m + 15) / 16;
   // Register-staged kernel: sub-chunks of 4 groups (int8: 2, to bound the

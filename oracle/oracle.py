@@ -210,9 +210,11 @@ def unpack_halfsplit(p):
 def pack_u32x8(codes):
     """codes [N, K] (0..15) -> uint32 [N, K/8]; element 8i+j in bits
     4j..4j+3 of word i."""
-    c = np.asarray(codes, dtype=np.uint32).reshape(np.shape(codes)[0], -1, 8)
-    shifts = (4 * np.arange(8, dtype=np.uint32))
-    return np.bitwise_or.reduce(c << shifts, axis=-1).astype(np.uint32)
+    # byte t of a little-endian word holds elements 2t (bits 8t..8t+3) and
+    # 2t+1 (bits 8t+4..8t+7)
+    c = np.asarray(codes, dtype=np.uint8).reshape(np.shape(codes)[0], -1)
+    pairs = np.ascontiguousarray(c[:, 0::2] | (c[:, 1::2] << 4))
+    return pairs.view("<u4").astype(np.uint32, copy=False)
 
 
 def unpack_u32x8(words):
@@ -339,10 +341,10 @@ def clib():
             raise RuntimeError(f"{path} missing: run make -C oracle")
         l = ctypes.CDLL(path)
         vp, i64 = ctypes.c_void_p, ctypes.c_int64
-        l.qo_matvec_int4_u32x8.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64,
-                                          ctypes.c_int, ctypes.c_int]
+        l.qo_matvec_int4_u32x8.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64,
+                                          i64, ctypes.c_int, ctypes.c_int]
         l.qo_matvec_int4_u32x8.restype = None
-        l.qo_matvec_u8.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64,
+        l.qo_matvec_u8.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64,
                                    ctypes.c_int, ctypes.c_int]
         l.qo_matvec_u8.restype = None
         l.qo_num_threads.restype = ctypes.c_int
@@ -356,9 +358,11 @@ def _ptr(a):
 
 
 def c_matvec_int4_u32x8(x_bf16_bits, words, s_bits, b_bits, group=GROUP,
-                        threads=0):
+                        threads=0, with_mag=False):
     """y (float32 [M, N]) = sum over groups of s*sum(x q) + b*sum(x) with
-    bf16 inputs given as uint16 bit arrays; words uint32 [N, K/8]."""
+    bf16 inputs given as uint16 bit arrays; words uint32 [N, K/8]. With
+    `with_mag`, returns (y, mag) where mag[m, o] = sum_k |x||s q + b|
+    (float64), the scale of an f32 product's rounding error."""
     x = np.ascontiguousarray(x_bf16_bits, dtype=np.uint16)
     w = np.ascontiguousarray(words, dtype=np.uint32)
     s = np.ascontiguousarray(s_bits, dtype=np.uint16)
@@ -366,12 +370,16 @@ def c_matvec_int4_u32x8(x_bf16_bits, words, s_bits, b_bits, group=GROUP,
     m, k = x.shape
     n = w.shape[0]
     y = np.zeros((m, n), dtype=np.float32)
+    mag = np.zeros((m, n), dtype=np.float64) if with_mag else None
     clib().qo_matvec_int4_u32x8(_ptr(x), _ptr(w), _ptr(s), _ptr(b), _ptr(y),
+                                None if mag is None else _ptr(mag),
                                 m, n, k, group, threads)
-    return y
+    return (y, mag) if with_mag else y
 
 
-def c_matvec_u8(x_bf16_bits, codes, s_bits, b_bits, group=GROUP, threads=0):
+def c_matvec_u8(x_bf16_bits, codes, s_bits, b_bits, group=GROUP, threads=0,
+                with_mag=False):
+    """As c_matvec_int4_u32x8 for affine uint8 codes [N, K]."""
     x = np.ascontiguousarray(x_bf16_bits, dtype=np.uint16)
     c = np.ascontiguousarray(codes, dtype=np.uint8)
     s = np.ascontiguousarray(s_bits, dtype=np.uint16)
@@ -379,9 +387,11 @@ def c_matvec_u8(x_bf16_bits, codes, s_bits, b_bits, group=GROUP, threads=0):
     m, k = x.shape
     n = c.shape[0]
     y = np.zeros((m, n), dtype=np.float32)
-    clib().qo_matvec_u8(_ptr(x), _ptr(c), _ptr(s), _ptr(b), _ptr(y), m, n, k,
-                        group, threads)
-    return y
+    mag = np.zeros((m, n), dtype=np.float64) if with_mag else None
+    clib().qo_matvec_u8(_ptr(x), _ptr(c), _ptr(s), _ptr(b), _ptr(y),
+                        None if mag is None else _ptr(mag), m, n, k, group,
+                        threads)
+    return (y, mag) if with_mag else y
 
 
 def c_threads(requested=0):

@@ -126,6 +126,33 @@ def test_half_index_limit_like_reference():
             assert st == _lib.UNIMPLEMENTED and "leading dimension" in msg
 
 
+def test_f32_sizes_beyond_int32_refused():
+    # The f32 kernels take 32-bit sizes: a dimension or leading dimension
+    # above INT32_MAX is refused (Unimplemented), never truncated.
+    big = (1 << 31) + 64
+    out = MatrixLayout("float32", 2, 2)
+    cfg = GemmConfig(MatrixLayout("float32", 2, 8, leading_dim_stride=big),
+                     MatrixLayout("float32", 8, 2), out, out)
+    st, msg = plan_status(cfg)
+    assert st == _lib.UNIMPLEMENTED and "leading dimension" in msg
+    cfg = GemmConfig(MatrixLayout("float32", 2, big), MatrixLayout("float32", big, 2),
+                     out, out)
+    st, msg = plan_status(cfg)
+    assert st == _lib.UNIMPLEMENTED and "dimension" in msg
+    for e in (Epilogue.kDefault, Epilogue.kBiasThenSILU):
+        out = MatrixLayout("float32", big, 2)
+        cfg = GemmConfig(MatrixLayout("float32", big, 4), MatrixLayout("float32", 4, 2),
+                         out, out)
+        st, msg = plan_status(cfg, e)
+        assert st == _lib.UNIMPLEMENTED and "f32 matmul too large" in msg
+    # just inside the limit is accepted
+    lim = (1 << 31) - 1
+    out = MatrixLayout("float32", 2, 2)
+    cfg = GemmConfig(MatrixLayout("float32", 2, 8, leading_dim_stride=lim),
+                     MatrixLayout("float32", 8, 2), out, out)
+    assert plan_status(cfg)[0] == _lib.OK
+
+
 def test_column_major_output_swaps_operands():
     out = MatrixLayout("bfloat16", 6, 10, Order.kColumnMajor)
     cfg = GemmConfig(MatrixLayout("bfloat16", 6, 4), MatrixLayout("bfloat16", 4, 10),
@@ -200,6 +227,77 @@ def test_ffi_argument_checks():
     # empty inputs are a no-op (no launch)
     ffi.rownorm(torch.zeros(0, 8), ffi.RownormKind.RMS)
     ffi.qmatvec(torch.zeros(0, 256, dtype=torch.bfloat16), words, s, s)
+
+
+def test_ffi_huge_dims_refused_without_overflow():
+    # Dimensions whose product overflows int64 are refused as invalid
+    # arguments, never wrapped into a count that passes the shape checks.
+    from qkern import ffi
+
+    def buf(dtype, dims, data=16):
+        b = _lib.BufferC()
+        b.data, b.dtype, b.rank = data, dtype, len(dims)
+        for i, d in enumerate(dims):
+            b.dims[i] = d
+        return b
+
+    attrs = _lib.QuantAttrsC(4, 64, int(ffi.Packing.U32X8), 1)
+    huge = 1 << 40
+    # x [2^40, 2^40] (2^80 elements, wraps to 0 in int64)
+    x = buf(_lib.BF16, [huge, huge])
+    codes = buf(_lib.U32, [8, huge // 8])
+    s = buf(_lib.BF16, [8, huge // 64])
+    y = buf(_lib.BF16, [huge, 8])
+    st = _lib.lib().qk_qmatvec(None, ctypes.byref(x), ctypes.byref(codes),
+                               ctypes.byref(s), ctypes.byref(s),
+                               ctypes.byref(y), ctypes.byref(attrs))
+    assert st == _lib.INVALID_ARGUMENT
+    assert b"2^56" in _lib.lib().qk_last_error_message()
+    # N * K overflows int64 while each buffer is in range: codes
+    # [2^35, 1] against K = 2^30 must not pass the element-count check.
+    x = buf(_lib.BF16, [1, 1 << 30])
+    codes = buf(_lib.U32, [1 << 35, 1])
+    st = _lib.lib().qk_qmatvec(None, ctypes.byref(x), ctypes.byref(codes),
+                               ctypes.byref(s), ctypes.byref(s),
+                               ctypes.byref(y), ctypes.byref(attrs))
+    assert st == _lib.INVALID_ARGUMENT
+    assert b"codes" in _lib.lib().qk_last_error_message()
+    # a zero dimension makes an empty buffer, whatever the others
+    r = buf(_lib.F32, [0, 1 << 62], data=0)
+    ra = _lib.RownormAttrsC(0, 1e-6, 0, 0)
+    assert _lib.lib().qk_rownorm(None, ctypes.byref(r), None, None,
+                                 ctypes.byref(r), ctypes.byref(ra)) == _lib.OK
+
+
+def test_unknown_dtype_refused_everywhere():
+    # A binding maps element types with no qk_dtype to -1 (INTEGRATION's
+    # ToQk); every target must refuse such a buffer, not reinterpret it.
+    from qkern import ffi
+    x = torch.zeros(1, 256, dtype=torch.bfloat16)
+    words = torch.zeros(8, 32, dtype=torch.int32)
+    s = torch.zeros(8, 4, dtype=torch.bfloat16)
+    y = torch.zeros(1, 8, dtype=torch.bfloat16)
+    attrs = _lib.QuantAttrsC(4, 64, int(ffi.Packing.U32X8), 1)
+    for pos in range(5):
+        bufs = [ffi.any_buffer(t) for t in (x, words, s, s, y)]
+        bufs[pos].dtype = -1
+        st = _lib.lib().qk_qmatvec(None, *[ctypes.byref(b) for b in bufs],
+                                   ctypes.byref(attrs))
+        assert st in (_lib.INVALID_ARGUMENT, _lib.UNIMPLEMENTED), pos
+    r = ffi.any_buffer(torch.zeros(2, 8))
+    r.dtype = -1
+    ra = _lib.RownormAttrsC(0, 1e-6, 0, 0)
+    assert _lib.lib().qk_rownorm(None, ctypes.byref(r), None, None,
+                                 ctypes.byref(r), ctypes.byref(ra)) == \
+        _lib.UNIMPLEMENTED
+    out = MatrixLayout("float32", 2, 2)
+    cfg = GemmConfig(MatrixLayout("float32", 2, 2), MatrixLayout("float32", 2, 2),
+                     out, out)
+    c = cfg.to_c()
+    c.lhs.dtype = c.rhs.dtype = -1
+    h = ctypes.c_void_p()
+    assert _lib.lib().qk_gemm_plan_create(ctypes.byref(c), 0, ctypes.byref(h)) \
+        == _lib.UNIMPLEMENTED
 
 
 def test_host_quantizer_matches_oracle():

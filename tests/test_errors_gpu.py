@@ -54,3 +54,48 @@ def test_host_argument_errors_are_not_sticky(dev):
     y = qkern.rms_norm(x, None, 1e-6)
     torch.cuda.synchronize()
     assert torch.isfinite(y.float()).all()
+
+
+@pytest.mark.parametrize("m,n", [(16, 4096), (64, 4096), (8, 151936)],
+                         ids=["ws", "wsmid", "wsp"])
+def test_wait_timeout_is_an_error_not_wrong_values(dev, m, n):
+    # The producer / consumer kernels (rows 5..16, 33..128 and the
+    # persistent lm_head form) wait on LDS flags with a bounded spin. A wait
+    # that gives up must surface as the sticky device error with NaN
+    # outputs, never as plausible values. QK_SPIN_LIMIT=0 makes every wait
+    # give up at once from the host side: no wait is left unbounded and
+    # every kernel still ends normally.
+    k = 4096
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16).to(dev)
+    words = torch.randint(-2**31, 2**31 - 1, (n, k // 8), dtype=torch.int32,
+                          generator=g).to(dev)
+    s = (torch.rand(n, k // 64, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    b = (torch.randn(n, k // 64, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    want = qkern.qmatvec(x, words, s, b)
+    torch.cuda.synchronize()
+    assert qkern.device_error() == 0
+    assert torch.isfinite(want.float()).all()
+    try:
+        os.environ["QK_SPIN_LIMIT"] = "0"
+        qkern.reset_device_error()  # re-reads the environment
+        y = qkern.qmatvec(x, words, s, b)  # the launch itself succeeds
+        torch.cuda.synchronize()
+        assert qkern.device_error() == _lib.INTERNAL
+        assert torch.isnan(y.float()).any()
+        # no finite output differs from the true one by more than rounding:
+        # a workgroup that gave up stores NaN for all its outputs
+        fin = torch.isfinite(y.float())
+        assert torch.equal(y[fin], want[fin])
+        with pytest.raises(qkern.QkError) as e:  # sticky
+            qkern.qmatvec(x, words, s, b)
+        assert "gave up waiting" in e.value.message
+    finally:
+        os.environ.pop("QK_SPIN_LIMIT", None)
+        torch.cuda.synchronize()
+        qkern.reset_device_error()
+    assert qkern.device_error() == 0
+    y = qkern.qmatvec(x, words, s, b)
+    torch.cuda.synchronize()
+    assert qkern.device_error() == 0
+    assert torch.equal(y, want)

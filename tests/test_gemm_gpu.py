@@ -381,28 +381,36 @@ def test_config_f32_1024_cubed(dev):
 @pytest.mark.parametrize("shape", [(4096, 4096, 4096), (2048, 12288, 4096),
                                    (2048, 4096, 12288)])
 def test_config_bf16_bias_silu(dev, shape):
+    # A, B ~ N(0,1)/sqrt(K) and bias ~ N(0, 0.02) from
+    # numpy default_rng seeds 0, 1 and 2, rounded to bf16.
     m, n, k = shape
-    g = torch.Generator(device="cpu").manual_seed(0)
-    a = (torch.randn(m, k, generator=g) / k ** 0.5).to(torch.bfloat16)
-    b = (torch.randn(k, n, generator=g) / k ** 0.5).to(torch.bfloat16)
-    bias = (0.02 * torch.randn(n, generator=g)).to(torch.bfloat16)
-    d = qkern.matmul(a.to(dev), b.to(dev), bias.to(dev),
+    a = O.bf16_round((np.random.default_rng(0).standard_normal(
+        (m, k), dtype=np.float32) / np.float32(k ** 0.5)))
+    b = O.bf16_round((np.random.default_rng(1).standard_normal(
+        (k, n), dtype=np.float32) / np.float32(k ** 0.5)))
+    bias = O.bf16_round(0.02 * np.random.default_rng(2).standard_normal(
+        n, dtype=np.float32))
+    d = qkern.matmul(torch.from_numpy(a).to(torch.bfloat16).to(dev),
+                     torch.from_numpy(b).to(torch.bfloat16).to(dev),
+                     torch.from_numpy(bias).to(torch.bfloat16).to(dev),
                      epilogue=Epilogue.kBiasThenSILU)
     torch.cuda.synchronize()
-    # float64 reference on a sample of rows (full product on the CPU in
-    # float64 is 137-206 GFLOP)
-    rows = np.r_[0:64, m - 64:m]
-    a64 = a.float().numpy().astype(np.float64)[rows]
-    want, _ = O.gemm_ref(a64, b.float().numpy(), None,
-                         bias.float().numpy(), act=3)
-    got = d[rows].float().cpu().numpy()
+    # float64 oracle on 512 rows (the full float64 product is 137-206
+    # GFLOP): the first and last 128 rows and a 256-row block across the
+    # middle tile boundary.
+    rows = np.r_[0:128, m // 2 - 128:m // 2 + 128, m - 128:m]
+    a64 = a[rows].astype(np.float64)
+    want, v = O.gemm_ref(a64, b, None, bias, act=3)
+    got = d[torch.from_numpy(rows).to(dev)].float().cpu().numpy()
+    assert np.all(np.isfinite(got))
     err = O.rel_fro(got, want)
     assert err <= 1e-2, err
-    # and all rows against torch's own bf16 GEMM (library, fp32 accumulate)
-    ref = torch.nn.functional.silu(a.to(dev).float() @ b.to(dev).float() +
-                                   bias.to(dev).float())
-    err_all = (d.float() - ref).norm() / ref.norm()
-    assert float(err_all) <= 1e-2
+    # elementwise: bf16 output rounding (2^-9 relative) plus f32
+    # accumulation, scaled by sum_k |a||b| (SiLU' is below 1.1)
+    mag = np.abs(a64) @ np.abs(b.astype(np.float64)) + np.abs(bias)
+    bound = 1e-2 * np.abs(want) + 1e-3 * mag
+    over = np.abs(got - want) - bound
+    assert np.all(over <= 0), float(over.max())
 
 
 @pytest.mark.parametrize("ta", [False, True])

@@ -269,6 +269,25 @@ def test_c_port_matvecs():
     # a dropped offset term would be caught:
     w_nob = O.dequantize_f32(codes.reshape(n, -1, 64), s[..., None])
     assert O.rel_fro(O.matvec_f64(x, w_nob), want) > 1e-2
+    # the magnitude output is sum_k |x||w| (numpy closed form), and the
+    # values returned with it are the same as without it
+    got_m, mag = O.c_matvec_int4_u32x8(O.bf16_bits(x), O.pack_u32x8(codes),
+                                       O.bf16_bits(s), O.bf16_bits(b),
+                                       threads=3, with_mag=True)
+    assert np.array_equal(got_m, got)
+    want_mag = np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T
+    assert np.allclose(mag, want_mag, rtol=1e-12)
+    got8m, mag8 = O.c_matvec_u8(O.bf16_bits(x), codes8, O.bf16_bits(s8),
+                                O.bf16_bits(b8), threads=1, with_mag=True)
+    assert np.array_equal(got8m, got8)
+    assert np.allclose(mag8, np.abs(x).astype(np.float64) @
+                       np.abs(w8).astype(np.float64).T, rtol=1e-12)
+    # each output row depends only on its own row of x (row order of the
+    # decode-once loop): swapping x's rows swaps y's rows exactly
+    got_sw = O.c_matvec_int4_u32x8(O.bf16_bits(x[::-1].copy()),
+                                   O.pack_u32x8(codes), O.bf16_bits(s),
+                                   O.bf16_bits(b), threads=2)
+    assert np.array_equal(got_sw, got[::-1])
 
 
 # ---------------------------------------------------------------------------
@@ -291,6 +310,27 @@ def test_rownorm_invariants():
     # softmax of two elements is a logistic function
     t = O.softmax(np.array([[0.3, -1.1]]))
     assert np.isclose(t[0, 0], 1 / (1 + math.exp(-1.4)), atol=1e-15)
+    # layer_norm with gain and beta: an affine map of the plain output,
+    # pinned by closed forms -- a constant row gives exactly beta (x - mean
+    # = 0), and a row of +-a (mean 0, variance a^2) gives gain * (+-a /
+    # sqrt(a^2 + eps)) + beta, which catches (y + beta) * gain.
+    gain = r.standard_normal(6) + 2.0
+    beta = r.standard_normal(6)
+    xc = np.full((2, 6), 7.5)
+    assert np.array_equal(O.layer_norm(xc, eps=1e-5, gain=gain, beta=beta),
+                          np.broadcast_to(beta, (2, 6)))
+    a, eps = 3.0, 0.25
+    xs = np.array([[a, -a, a, -a, a, -a]])
+    sign = np.array([1, -1, 1, -1, 1, -1], dtype=np.float64)
+    want = gain * sign * a / math.sqrt(a * a + eps) + beta
+    assert np.allclose(O.layer_norm(xs, eps=eps, gain=gain, beta=beta), want,
+                       atol=1e-14)
+    assert not np.allclose((O.layer_norm(xs, eps=eps) + beta) * gain, want)
+    # gain alone scales and beta alone shifts the plain output
+    y0 = O.layer_norm(x, eps=1e-5)
+    g1 = r.standard_normal(1000)
+    assert np.allclose(O.layer_norm(x, eps=1e-5, gain=g1), y0 * g1, atol=1e-14)
+    assert np.allclose(O.layer_norm(x, eps=1e-5, beta=g1), y0 + g1, atol=1e-14)
     # rms_norm's defining identity: mean(y^2) = mean(x^2)/(mean(x^2)+eps)
     y = O.rms_norm(x, eps=0.5)
     ms = (x * x).mean(-1)

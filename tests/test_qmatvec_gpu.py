@@ -343,55 +343,84 @@ def test_dequantize_f32_scale_rounding_unfused(dev):
 
 QWEN3_8B = [(4096, 4096), (12288, 4096), (4096, 12288), (151936, 4096)]
 
-
-@pytest.mark.parametrize("nk", QWEN3_8B)
-def test_config_int4_decode(dev, nk):
-    n, k = nk
-    codes, s, b = O.config_affine(n, k, bits=4, seed=0)
-    words = O.pack_u32x8(codes)
-    rng = np.random.default_rng(1)
-    x = O.bf16_round(rng.standard_normal((1, k)).astype(np.float32))
-    y = qkern.qmatvec(torch.from_numpy(x).to(torch.bfloat16).to(dev),
-                      torch.from_numpy(words.view(np.int32)).to(dev),
-                      torch.from_numpy(s).to(torch.bfloat16).to(dev),
-                      torch.from_numpy(b).to(torch.bfloat16).to(dev))
-    torch.cuda.synchronize()
-    want = O.c_matvec_int4_u32x8(O.bf16_bits(x), words, O.bf16_bits(s),
-                                 O.bf16_bits(b))
-    assert O.rel_fro(y.float().cpu().numpy(), want) <= 1e-2
+_CONFIG_CACHE = {}
 
 
-@pytest.mark.parametrize("m", [16, 512])
-def test_config_int4_batched(dev, m):
-    n, k = 12288, 4096
-    codes, s, b = O.config_affine(n, k, bits=4, seed=0)
-    words = O.pack_u32x8(codes)
-    rng = np.random.default_rng(2)
+def config_weights(dev, n, k, bits):
+    """BASELINE config weights (seed 0) as host bit arrays for the C port
+    and device tensors for qkern, built once per shape (the lm_head's
+    codes take seconds to draw)."""
+    key = (n, k, bits)
+    if key not in _CONFIG_CACHE:
+        if len(_CONFIG_CACHE) >= 2:  # bound host and device memory
+            _CONFIG_CACHE.pop(next(iter(_CONFIG_CACHE)))
+        codes, s, b = O.config_affine(n, k, bits=bits, seed=0)
+        host = O.pack_u32x8(codes) if bits == 4 else codes
+        dcodes = torch.from_numpy(host.view(np.int32) if bits == 4 else host)
+        _CONFIG_CACHE[key] = dict(
+            host=host, s_bits=O.bf16_bits(s), b_bits=O.bf16_bits(b),
+            dcodes=dcodes.to(dev),
+            ds=torch.from_numpy(s).to(torch.bfloat16).to(dev),
+            db=torch.from_numpy(b).to(torch.bfloat16).to(dev))
+    return _CONFIG_CACHE[key]
+
+
+def check_config(got, want, mag, tol=1e-2):
+    """Elementwise bound against the C port (float32, the reference's
+    factoring): |got - want| <= tol |want| + 1e-3 sum_k |x||w| for every
+    checked output, plus the relative Frobenius error."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert np.all(np.isfinite(got))
+    assert O.rel_fro(got, want) <= tol
+    err = np.abs(got - want)
+    bound = tol * np.abs(want) + 1e-3 * mag
+    bad = np.argwhere(err > bound)
+    assert bad.size == 0, (bad[:5].tolist(), float(np.max(err - bound)))
+
+
+def run_config_int4(dev, m, n, k, rows, seed):
+    wts = config_weights(dev, n, k, 4)
+    rng = np.random.default_rng(seed)
     x = O.bf16_round(rng.standard_normal((m, k)).astype(np.float32))
     y = qkern.qmatvec(torch.from_numpy(x).to(torch.bfloat16).to(dev),
-                      torch.from_numpy(words.view(np.int32)).to(dev),
-                      torch.from_numpy(s).to(torch.bfloat16).to(dev),
-                      torch.from_numpy(b).to(torch.bfloat16).to(dev))
+                      wts["dcodes"], wts["ds"], wts["db"])
     torch.cuda.synchronize()
-    rows = sorted(set([0, 1, m // 2, m - 1]))
-    want = O.c_matvec_int4_u32x8(O.bf16_bits(x[rows]), words, O.bf16_bits(s),
-                                 O.bf16_bits(b))
-    assert O.rel_fro(y.float().cpu().numpy()[rows], want) <= 1e-2
+    want, mag = O.c_matvec_int4_u32x8(O.bf16_bits(x[rows]), wts["host"],
+                                      wts["s_bits"], wts["b_bits"],
+                                      with_mag=True)
+    check_config(y.float().cpu().numpy()[rows], want, mag)
+
+
+def config_rows(m):
+    """Rows checked at a config: all of them up to 128; beyond, one full
+    128-row block that crosses the 256-row tile boundary, plus the first
+    and last rows."""
+    if m <= 128:
+        return np.arange(m)
+    return np.r_[0, 192:320, m - 1]
+
+
+@pytest.mark.parametrize("m", [1, 16, 512])
+@pytest.mark.parametrize("nk", QWEN3_8B, ids=[f"{n}x{k}" for n, k in QWEN3_8B])
+def test_config_int4(dev, nk, m):
+    # BASELINE config C5: every shape at M = 1 (decode), 16 and 512
+    # (prefill; the lm_head at M = 512 is a 637 GFLOP fused dequantize +
+    # MFMA GEMM).
+    n, k = nk
+    run_config_int4(dev, m, n, k, config_rows(m), seed={1: 1}.get(m, 2))
 
 
 @pytest.mark.parametrize("m", [1, 8, 128])
 def test_config_int8_affine(dev, m):
     n, k = 12288, 4096
-    codes, s, b = O.config_affine(n, k, bits=8, seed=0)
+    wts = config_weights(dev, n, k, 8)
     rng = np.random.default_rng(3)
     x = O.bf16_round(rng.standard_normal((m, k)).astype(np.float32))
     y = qkern.qmatvec(torch.from_numpy(x).to(torch.bfloat16).to(dev),
-                      torch.from_numpy(codes).to(dev),
-                      torch.from_numpy(s).to(torch.bfloat16).to(dev),
-                      torch.from_numpy(b).to(torch.bfloat16).to(dev),
-                      packing=Packing.U8)
+                      wts["dcodes"], wts["ds"], wts["db"], packing=Packing.U8)
     torch.cuda.synchronize()
-    rows = sorted(set([0, m // 2, m - 1]))
-    want = O.c_matvec_u8(O.bf16_bits(x[rows]), codes, O.bf16_bits(s),
-                         O.bf16_bits(b))
-    assert O.rel_fro(y.float().cpu().numpy()[rows], want) <= 1e-2
+    rows = config_rows(m)
+    want, mag = O.c_matvec_u8(O.bf16_bits(x[rows]), wts["host"],
+                              wts["s_bits"], wts["b_bits"], with_mag=True)
+    check_config(y.float().cpu().numpy()[rows], want, mag)
