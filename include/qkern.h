@@ -46,7 +46,7 @@ typedef enum {
 } qk_status;
 
 /* Element types. F32/F16/BF16 are GEMM and activation types; U8, S8 and
- * U32 hold quantized codes. */
+ * U32 hold quantized codes; S32 (or U32) holds the decode position. */
 typedef enum {
   QK_F32 = 0,
   QK_F16 = 1,
@@ -54,6 +54,7 @@ typedef enum {
   QK_U8 = 3,
   QK_S8 = 4,
   QK_U32 = 5,
+  QK_S32 = 6,
 } qk_dtype;
 
 /* ------------------------------------------------------------------------
@@ -235,6 +236,44 @@ typedef struct {
 qk_status qk_rownorm(void* stream, const qk_buffer* x, const qk_buffer* gain,
                      const qk_buffer* beta, qk_buffer* y,
                      const qk_rownorm_attrs* attrs);
+
+/* Attributes of the qk$decode_attention target. */
+typedef struct {
+  float scale;    /* multiplies q.k; the reference uses head_dim ** -0.5 */
+  int32_t window; /* S: cache slots [0, S) are attended where s <= position;
+                     0 means the whole cache (Smax) */
+} qk_attention_attrs;
+
+/* Workspace bytes qk_decode_attention needs for these shapes: partial
+ * (max, sum, accumulator) rows of the split cache window, f32. */
+qk_status qk_decode_attention_workspace_size(const qk_buffer* q,
+                                             const qk_buffer* k_cache,
+                                             const qk_attention_attrs* attrs,
+                                             uint64_t* bytes);
+
+/* Target qk$decode_attention: grouped-query attention of one query per
+ * sequence against the KV cache, as the one-query branch of the
+ * reference's attention() (examples/llm/qwen3.py:322-326) computes it with
+ * forward()'s decode mask (qwen3.py:357-358), replacing the reductions XLA
+ * emits for it:
+ *   q [B, KV, G, D] (or [B, 1, KV, G, D]), k_cache [B, KV, Smax, D],
+ *   v_cache [B, KV, D, Smax] (the layouts of init_cache, qwen3.py:
+ *   279-291), position: int32 device scalar (1 element, S32 or U32);
+ *   t[s] = scale * sum_d q[d] k[s, d] for slots s < window with s <= pos,
+ *   p = softmax(t), out[g, d] = sum_s p[s] v[d, s]
+ * in f32, rounded once into out (q's shape and type). q, caches and out
+ * are all bf16 or all f16; D is 64 or 128; G <= 16; Smax a multiple of 8;
+ * buffers 16-byte aligned. The position is read on the device (a jitted
+ * decode loop passes it as a traced value); slots past min(window, pos + 1)
+ * are not read. `workspace` (device memory of at least
+ * qk_decode_attention_workspace_size bytes, contents ignored, clobbered)
+ * holds the partials of the split window. */
+qk_status qk_decode_attention(void* stream, const qk_buffer* q,
+                              const qk_buffer* k_cache,
+                              const qk_buffer* v_cache,
+                              const qk_buffer* position, qk_buffer* out,
+                              const qk_attention_attrs* attrs,
+                              void* workspace, uint64_t workspace_bytes);
 
 /* ------------------------------------------------------------------------
  * Status.

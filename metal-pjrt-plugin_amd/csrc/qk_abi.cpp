@@ -165,6 +165,7 @@ int DTypeSize(int dtype) {
   switch (dtype) {
     case QK_F32:
     case QK_U32:
+    case QK_S32:
       return 4;
     case QK_F16:
     case QK_BF16:
@@ -190,6 +191,8 @@ const char* DTypeName(int dtype) {
       return "s8";
     case QK_U32:
       return "u32";
+    case QK_S32:
+      return "s32";
   }
   return "?";
 }
@@ -858,6 +861,161 @@ extern "C" qk_status qk_rownorm(void* stream, const qk_buffer* x,
   if (r.rows == 0 || r.n == 0) return QK_OK;
   if (qk_status s = qk::PreLaunch(); s != QK_OK) return s;
   return qk::LaunchRownorm(r, static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// qk$decode_attention.
+
+namespace {
+
+// Checks of qk$decode_attention's q and key cache and attributes; fills the
+// problem's shapes and plan.
+qk_status CheckAttentionShapes(const qk_buffer* q, const qk_buffer* k,
+                               const qk_attention_attrs* attrs,
+                               qk::AttentionProblem* p) {
+  if (attrs == nullptr) return Fail(QK_INVALID_ARGUMENT, "qkern: null attrs");
+  if (qk_status s = CheckBuffer(q, "q", false); s != QK_OK) return s;
+  if (qk_status s = CheckBuffer(k, "k_cache", false); s != QK_OK) return s;
+  // q [B, KV, G, D] or the reference's [B, 1, KV, G, D]
+  const bool q5 = q->rank == 5 && q->dims[1] == 1;
+  if (q->rank != 4 && !q5) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: decode attention q must be [B, KV, G, D] or "
+                "[B, 1, KV, G, D], got " +
+                    BufferString(*q));
+  }
+  const int64_t* qd = q5 ? q->dims + 1 : q->dims;
+  p->b = q->dims[0];
+  p->kv = qd[1];
+  p->g = qd[2];
+  p->d = qd[3];
+  if (q->dtype != QK_BF16 && q->dtype != QK_F16) {
+    return Fail(QK_UNIMPLEMENTED,
+                "qkern: decode attention takes bf16 or f16 q and caches, "
+                "got q " +
+                    BufferString(*q));
+  }
+  if (p->d != 64 && p->d != 128) {
+    return Fail(QK_UNIMPLEMENTED, "qkern: decode attention head dim " +
+                                      std::to_string(p->d) +
+                                      " is not supported (64 or 128)");
+  }
+  if (p->g < 1 || p->g > 16) {
+    return Fail(QK_UNIMPLEMENTED,
+                "qkern: decode attention with " + std::to_string(p->g) +
+                    " query heads per KV head is not supported (1 to 16)");
+  }
+  if (k->rank != 4 || k->dtype != q->dtype || k->dims[0] != p->b ||
+      k->dims[1] != p->kv || k->dims[3] != p->d) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: k_cache must be " +
+                    std::string(qk::DTypeName(q->dtype)) + " [" +
+                    std::to_string(p->b) + ", " + std::to_string(p->kv) +
+                    ", Smax, " + std::to_string(p->d) + "], got " +
+                    BufferString(*k));
+  }
+  p->smax = k->dims[2];
+  if (p->smax % 8 != 0 || p->smax > (int64_t{1} << 24)) {
+    return Fail(QK_UNIMPLEMENTED,
+                "qkern: decode attention needs a cache length that is a "
+                "multiple of 8 and at most 2^24, got " +
+                    std::to_string(p->smax));
+  }
+  const int64_t window = attrs->window == 0 ? p->smax : attrs->window;
+  if (window < 0 || window > p->smax) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: attention window " + std::to_string(attrs->window) +
+                    " outside the cache length " + std::to_string(p->smax));
+  }
+  p->window = window;
+  p->scale = attrs->scale;
+  p->dtype = q->dtype;
+  if (p->b > 0 && p->kv > 0 && p->window > 0) qk::PlanAttention(p);
+  return QK_OK;
+}
+
+}  // namespace
+
+extern "C" qk_status qk_decode_attention_workspace_size(
+    const qk_buffer* q, const qk_buffer* k_cache,
+    const qk_attention_attrs* attrs, uint64_t* bytes) {
+  if (bytes == nullptr) return Fail(QK_INVALID_ARGUMENT, "qkern: null bytes");
+  *bytes = 0;
+  qk::AttentionProblem p;
+  if (qk_status s = CheckAttentionShapes(q, k_cache, attrs, &p); s != QK_OK)
+    return s;
+  *bytes = p.workspace_bytes;
+  return QK_OK;
+}
+
+extern "C" qk_status qk_decode_attention(
+    void* stream, const qk_buffer* q, const qk_buffer* k_cache,
+    const qk_buffer* v_cache, const qk_buffer* position, qk_buffer* out,
+    const qk_attention_attrs* attrs, void* workspace,
+    uint64_t workspace_bytes) {
+  qk::AttentionProblem p;
+  if (qk_status s = CheckAttentionShapes(q, k_cache, attrs, &p); s != QK_OK)
+    return s;
+  if (qk_status s = CheckBuffer(v_cache, "v_cache", false); s != QK_OK)
+    return s;
+  if (qk_status s = CheckBuffer(out, "out", false); s != QK_OK) return s;
+  if (v_cache->rank != 4 || v_cache->dtype != p.dtype ||
+      v_cache->dims[0] != p.b || v_cache->dims[1] != p.kv ||
+      v_cache->dims[2] != p.d || v_cache->dims[3] != p.smax) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: v_cache must be " +
+                    std::string(qk::DTypeName(p.dtype)) + " [" +
+                    std::to_string(p.b) + ", " + std::to_string(p.kv) +
+                    ", " + std::to_string(p.d) + ", " +
+                    std::to_string(p.smax) + "], got " +
+                    BufferString(*v_cache));
+  }
+  bool same = out->rank == q->rank && out->dtype == p.dtype;
+  for (int i = 0; same && i < q->rank; ++i) same = out->dims[i] == q->dims[i];
+  if (!same) {
+    return Fail(QK_INVALID_ARGUMENT, "qkern: decode attention output " +
+                                         BufferString(*out) +
+                                         " must match q " + BufferString(*q));
+  }
+  if (position == nullptr || position->rank > 1 ||
+      (position->rank == 1 && position->dims[0] != 1) ||
+      (position->dtype != QK_S32 && position->dtype != QK_U32) ||
+      position->data == nullptr) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: decode attention position must be one int32 on the "
+                "device");
+  }
+  if (p.b == 0 || p.kv == 0) return QK_OK;
+  if (p.window == 0) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: decode attention over an empty cache window");
+  }
+  for (const void* ptr : {static_cast<const void*>(q->data),
+                          static_cast<const void*>(k_cache->data),
+                          static_cast<const void*>(v_cache->data),
+                          static_cast<const void*>(out->data)}) {
+    if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0) {
+      return Fail(QK_INVALID_ARGUMENT,
+                  "qkern: decode attention buffers must be 16-byte aligned");
+    }
+  }
+  if (workspace == nullptr || workspace_bytes < p.workspace_bytes) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: decode attention needs a workspace of " +
+                    std::to_string(p.workspace_bytes) + " bytes, got " +
+                    std::to_string(workspace_bytes));
+  }
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: decode attention workspace must be 16-byte aligned");
+  }
+  p.q = q->data;
+  p.k = k_cache->data;
+  p.v = v_cache->data;
+  p.pos = position->data;
+  p.out = out->data;
+  if (qk_status s = qk::PreLaunch(); s != QK_OK) return s;
+  return qk::LaunchAttention(p, workspace, static_cast<hipStream_t>(stream));
 }
 
 // ---------------------------------------------------------------------------

@@ -138,4 +138,27 @@ struct RownormProblem {
 
 qk_status LaunchRownorm(const RownormProblem& p, hipStream_t stream);
 
+// ---------------------------------------------------------------------------
+// Decode attention (attention.hip).
+
+struct AttentionProblem {
+  int64_t b = 0, kv = 0, g = 0, d = 0;  // q [b, kv, g, d]
+  int64_t smax = 0, window = 0;         // cache slots, slots read
+  float scale = 1.f;
+  int dtype = QK_BF16;                  // q, caches and output
+  const void* q = nullptr;
+  const void* k = nullptr;  // [b, kv, smax, d]
+  const void* v = nullptr;  // [b, kv, d, smax]
+  const void* pos = nullptr;  // int32 device scalar
+  void* out = nullptr;        // [b, kv, g, d]
+  // Set by PlanAttention: chunks of 64 slots per wave, partials per (b, kv)
+  // and the workspace they take.
+  int cpw = 1, parts = 0;
+  uint64_t workspace_bytes = 0;
+};
+
+void PlanAttention(AttentionProblem* p);
+qk_status LaunchAttention(const AttentionProblem& p, void* workspace,
+                          hipStream_t stream);
+
 }  // namespace qk

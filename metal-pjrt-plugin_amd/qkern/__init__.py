@@ -3,7 +3,8 @@
 Three kernel families behind a C ABI (include/qkern.h, libqkern.so):
   - blas:  BlasLt matmul plans, f32/f16/bf16 with the cuBLASLt epilogue;
   - ffi:   qk$qmatvec / qk$dequantize (int4 / int8 group-affine weights)
-           and qk$rownorm (RMSNorm, LayerNorm, softmax);
+           qk$rownorm (RMSNorm, LayerNorm, softmax) and
+           qk$decode_attention (one query against the KV cache);
   - quant: host-side quantizers and packers for the weight formats.
 Every compute call runs a HIP kernel; there is no CPU fallback.
 """
@@ -11,7 +12,8 @@ Every compute call runs a HIP kernel; there is no CPU fallback.
 from ._lib import QkError, lib  # noqa: F401
 from .blas import (BlasLt, Epilogue, GemmConfig, MatmulPlan,  # noqa: F401
                    MatrixLayout, MemoryArgs, Order, matmul)
-from .ffi import (Packing, RownormKind, dequantize, layer_norm,  # noqa: F401
+from .ffi import (Packing, RownormKind, decode_attention,  # noqa: F401
+                  decode_attention_workspace_size, dequantize, layer_norm,
                   qmatvec, rms_norm, rownorm, softmax)
 
 

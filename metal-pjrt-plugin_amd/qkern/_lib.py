@@ -15,7 +15,7 @@ STATUS_NAMES = {0: "OK", 3: "INVALID_ARGUMENT", 8: "RESOURCE_EXHAUSTED",
                 12: "UNIMPLEMENTED", 13: "INTERNAL"}
 
 # qk_dtype
-F32, F16, BF16, U8, S8, U32 = 0, 1, 2, 3, 4, 5
+F32, F16, BF16, U8, S8, U32, S32 = 0, 1, 2, 3, 4, 5, 6
 
 MAX_RANK = 6
 
@@ -56,6 +56,10 @@ class QuantAttrsC(ctypes.Structure):
                 ("packing", ctypes.c_int32), ("has_bias", ctypes.c_int32)]
 
 
+class AttentionAttrsC(ctypes.Structure):
+    _fields_ = [("scale", ctypes.c_float), ("window", ctypes.c_int32)]
+
+
 class RownormAttrsC(ctypes.Structure):
     _fields_ = [("kind", ctypes.c_int32), ("eps", ctypes.c_float),
                 ("has_gain", ctypes.c_int32), ("has_beta", ctypes.c_int32)]
@@ -79,6 +83,14 @@ SIGNATURES = {
     "qk_rownorm": (ctypes.c_int, [ctypes.c_void_p, _P(BufferC), _P(BufferC),
                                   _P(BufferC), _P(BufferC),
                                   _P(RownormAttrsC)]),
+    "qk_decode_attention_workspace_size": (
+        ctypes.c_int, [_P(BufferC), _P(BufferC), _P(AttentionAttrsC),
+                       _P(ctypes.c_uint64)]),
+    "qk_decode_attention": (ctypes.c_int, [ctypes.c_void_p, _P(BufferC),
+                                           _P(BufferC), _P(BufferC),
+                                           _P(BufferC), _P(BufferC),
+                                           _P(AttentionAttrsC),
+                                           ctypes.c_void_p, ctypes.c_uint64]),
     "qk_last_error_message": (ctypes.c_char_p, []),
     "qk_device_error": (ctypes.c_int, []),
     "qk_reset_device_error": (None, []),

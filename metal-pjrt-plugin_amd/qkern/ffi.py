@@ -1,4 +1,5 @@
-"""Typed-FFI style targets: qk$qmatvec, qk$dequantize, qk$rownorm.
+"""Typed-FFI style targets: qk$qmatvec, qk$dequantize, qk$rownorm,
+qk$decode_attention.
 
 The reference has no custom-call target for these (XLA fuses the JAX code
 of examples/llm/qwen3.py into reduction kernels). They follow the
@@ -125,3 +126,45 @@ def layer_norm(x, eps=1e-5, gain=None, beta=None):
     """(x - mean) / sqrt(var + eps) [* gain + beta] over the last axis
     (bench/jax_bench.py:44-46 without the affine terms)."""
     return rownorm(x, RownormKind.LAYER, eps=eps, gain=gain, beta=beta)
+
+
+def decode_attention_workspace_size(q, k_cache, *, scale=None, window=0):
+    """Bytes of workspace qk$decode_attention takes for these shapes."""
+    attrs = _attn_attrs(q, scale, window)
+    n = ctypes.c_uint64()
+    check(lib().qk_decode_attention_workspace_size(
+        _ref(any_buffer(q)), _ref(any_buffer(k_cache)), ctypes.byref(attrs),
+        ctypes.byref(n)))
+    return n.value
+
+
+def _attn_attrs(q, scale, window):
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    return _lib.AttentionAttrsC(float(scale), int(window or 0))
+
+
+def decode_attention(q, k_cache, v_cache, position, *, scale=None, window=0,
+                     workspace=None, out=None, stream=None):
+    """qk$decode_attention: qwen3.attention for one query
+    (examples/llm/qwen3.py:322-326) with the decode mask s <= position over
+    cache slots s < window (0: all). q [B, KV, G, D] or [B, 1, KV, G, D],
+    k_cache [B, KV, Smax, D], v_cache [B, KV, D, Smax], position an int32
+    device tensor of one element. scale defaults to D ** -0.5 (the
+    reference's). A workspace is allocated when none is given."""
+    attrs = _attn_attrs(q, scale, window)
+    if out is None:
+        out = torch.empty_like(q, dtype=v_cache.dtype)
+    if workspace is None:
+        need = decode_attention_workspace_size(q, k_cache, scale=scale,
+                                               window=window)
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8,
+                                device=q.device)
+    pos = position.reshape(1) if position.dim() == 0 else position
+    bq, bk, bv, bp, bo = (any_buffer(t) for t in (q, k_cache, v_cache, pos,
+                                                   out))
+    check(lib().qk_decode_attention(
+        stream_handle(stream), _ref(bq), _ref(bk), _ref(bv), _ref(bp),
+        _ref(bo), ctypes.byref(attrs), workspace.data_ptr(),
+        workspace.numel() * workspace.element_size()))
+    return out

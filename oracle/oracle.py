@@ -303,6 +303,24 @@ def softmax(x):
     return e / e.sum(axis=-1, keepdims=True)
 
 
+def decode_attention(q, k, v, pos, scale, window=None):
+    """The one-query branch of qwen3.attention (examples/llm/qwen3.py:
+    322-326) with forward()'s decode mask (qwen3.py:357-358), in float64:
+    q [B, KV, G, D], k [B, KV, Smax, D], v [B, KV, D, Smax]; slots
+    s < window (default Smax) with s <= pos are attended:
+      t = scale * q.k,  p = softmax(t over attended slots),  o = p.v
+    Returns [B, KV, G, D]."""
+    q = np.asarray(q, dtype=np.float64)
+    S = window or np.shape(k)[2]
+    k = np.asarray(k, dtype=np.float64)[:, :, :S]
+    v = np.asarray(v, dtype=np.float64)[..., :S]
+    t = np.einsum("bkgd,bksd->bkgs", q, k) * scale
+    t = np.where(np.arange(S) <= pos, t, -np.inf)
+    with np.errstate(invalid="ignore"):
+        p = softmax(t)
+    return np.einsum("bkgs,bkds->bkgd", p, v)
+
+
 # ---------------------------------------------------------------------------
 # Seeded inputs of the benchmark configs (numpy default_rng(seed)).
 

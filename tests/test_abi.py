@@ -319,3 +319,54 @@ def test_host_quantizer_matches_oracle():
     assert np.array_equal(q8, oq8.reshape(24, -1))
     assert np.array_equal(s8, os8.reshape(24, -1))
     assert np.array_equal(quant.to_bf16_bits(w), O.bf16_bits(w))
+
+
+def test_decode_attention_argument_checks():
+    # shapes, types and workspace are checked before any launch (host
+    # tensors stand in for device buffers here)
+    q = torch.zeros(1, 8, 4, 128, dtype=torch.bfloat16)
+    k = torch.zeros(1, 8, 64, 128, dtype=torch.bfloat16)
+    v = torch.zeros(1, 8, 128, 64, dtype=torch.bfloat16)
+    pos = torch.zeros(1, dtype=torch.int32)
+    need = qkern.decode_attention_workspace_size(q, k)
+    # one partial per 64-slot chunk: (D accumulators + max + sum) f32 per
+    # query head
+    assert need == 8 * 1 * 4 * (128 + 2) * 4
+
+    def status(fn):
+        try:
+            fn()
+            return _lib.OK, ""
+        except qkern.QkError as e:
+            return e.status, e.message
+
+    ws = torch.zeros(need, dtype=torch.uint8)
+    st, msg = status(lambda: qkern.decode_attention(
+        q, k, v, pos, workspace=ws[:need - 4]))
+    assert st == _lib.INVALID_ARGUMENT and "workspace" in msg
+    st, msg = status(lambda: qkern.decode_attention(
+        q, k, v.transpose(2, 3).contiguous(), pos, workspace=ws))
+    assert st == _lib.INVALID_ARGUMENT and "v_cache" in msg
+    st, msg = status(lambda: qkern.decode_attention(
+        q.float(), k.float(), v.float(), pos, workspace=ws))
+    assert st == _lib.UNIMPLEMENTED
+    st, msg = status(lambda: qkern.decode_attention(
+        q, k, v, pos.float(), workspace=ws))
+    assert st == _lib.INVALID_ARGUMENT and "position" in msg
+    st, msg = status(lambda: qkern.decode_attention(
+        q, k, v, pos, window=65, workspace=ws))
+    assert st == _lib.INVALID_ARGUMENT and "window" in msg
+    q96 = torch.zeros(1, 8, 4, 96, dtype=torch.bfloat16)
+    st, msg = status(lambda: qkern.decode_attention_workspace_size(
+        q96, torch.zeros(1, 8, 64, 96, dtype=torch.bfloat16)))
+    assert st == _lib.UNIMPLEMENTED and "head dim" in msg
+    st, msg = status(lambda: qkern.decode_attention_workspace_size(
+        q, torch.zeros(1, 8, 60, 128, dtype=torch.bfloat16)))
+    assert st == _lib.UNIMPLEMENTED and "multiple of 8" in msg
+    # long windows run several chunks per wave: fewer partials
+    kl = torch.zeros(1, 8, 32768, 128, dtype=torch.bfloat16)
+    assert qkern.decode_attention_workspace_size(q, kl) == \
+        8 * 256 * 4 * (128 + 2) * 4
+    # an empty batch launches nothing
+    qkern.decode_attention(q[:0], k[:0], v[:0], pos,
+                           workspace=torch.zeros(16, dtype=torch.uint8))

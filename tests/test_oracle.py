@@ -355,3 +355,57 @@ def test_quantize_groups(group):
     codes, s, b = O.quantize_int4(w, group)
     assert codes.shape == (4, 256 // group, group)
     assert O.rel_fro(O.dequantize_f32(codes, s, b), w) < 0.2
+
+
+# ---------------------------------------------------------------------------
+# decode attention
+
+
+def attention_bruteforce(q, k, v, pos, scale, window):
+    """Loops over heads and slots (pins O.decode_attention on tiny
+    shapes): explicit max-subtracted exponentials and weighted sums."""
+    B, KV, G, D = q.shape
+    out = np.zeros((B, KV, G, D))
+    for b in range(B):
+        for h in range(KV):
+            for g in range(G):
+                slots = [s for s in range(window) if s <= pos]
+                t = [scale * sum(float(q[b, h, g, d]) * float(k[b, h, s, d])
+                                 for d in range(D)) for s in slots]
+                m = max(t)
+                e = [math.exp(x - m) for x in t]
+                z = sum(e)
+                for d in range(D):
+                    out[b, h, g, d] = sum(e[i] * float(v[b, h, d, s])
+                                          for i, s in enumerate(slots)) / z
+    return out
+
+
+def test_decode_attention_oracle():
+    r = np.random.default_rng(21)
+    B, KV, G, D, Smax = 2, 2, 3, 4, 8
+    q = r.standard_normal((B, KV, G, D))
+    k = r.standard_normal((B, KV, Smax, D))
+    v = r.standard_normal((B, KV, D, Smax))
+    for pos, window in [(0, 8), (3, 8), (7, 8), (9, 6), (4, 5)]:
+        got = O.decode_attention(q, k, v, pos, 0.7, window)
+        want = attention_bruteforce(q, k, v, pos, 0.7, window)
+        assert np.allclose(got, want, atol=1e-12), (pos, window)
+    # closed forms: one attended slot returns that slot's values; equal
+    # keys (or scale 0) give the mean of the attended values; a key far
+    # more aligned than the rest selects its slot
+    one = O.decode_attention(q, k, v, 0, 0.5)
+    assert np.allclose(one, np.broadcast_to(v[:, :, None, :, 0], one.shape))
+    kc = np.broadcast_to(k[:, :, :1], k.shape)
+    mean = O.decode_attention(q, kc, v, 5, 0.9)
+    assert np.allclose(mean, np.broadcast_to(
+        v[:, :, None, :, :6].mean(-1), mean.shape), atol=1e-12)
+    assert np.allclose(O.decode_attention(q, k, v, 5, 0.0), mean, atol=1e-12)
+    kb = k.copy()
+    kb[:, :, 2] = 50.0 * q[:, :, 0]  # slot 2 aligned with head 0
+    sel = O.decode_attention(q, kb, v, 7, 1.0)
+    assert np.allclose(sel[:, :, 0], v[:, :, :, 2], atol=1e-9)
+    # a transposed value cache (the [B, KV, S, D] layout of keys) or a
+    # dropped scale would be caught
+    assert not np.allclose(O.decode_attention(q, k, v, 7, 0.7),
+                           O.decode_attention(q, k, v, 7, 1.0))
