@@ -948,12 +948,15 @@ extern "C" qk_status qk_decode_attention_workspace_size(
   return QK_OK;
 }
 
-extern "C" qk_status qk_decode_attention(
-    void* stream, const qk_buffer* q, const qk_buffer* k_cache,
-    const qk_buffer* v_cache, const qk_buffer* position, qk_buffer* out,
-    const qk_attention_attrs* attrs, void* workspace,
-    uint64_t workspace_bytes) {
-  qk::AttentionProblem p;
+namespace {
+
+// Every check of qk$decode_attention except the workspace's; fills p.
+qk_status CheckAttention(const qk_buffer* q, const qk_buffer* k_cache,
+                         const qk_buffer* v_cache, const qk_buffer* position,
+                         const qk_buffer* out,
+                         const qk_attention_attrs* attrs,
+                         qk::AttentionProblem* pp) {
+  qk::AttentionProblem& p = *pp;
   if (qk_status s = CheckAttentionShapes(q, k_cache, attrs, &p); s != QK_OK)
     return s;
   if (qk_status s = CheckBuffer(v_cache, "v_cache", false); s != QK_OK)
@@ -999,6 +1002,27 @@ extern "C" qk_status qk_decode_attention(
                   "qkern: decode attention buffers must be 16-byte aligned");
     }
   }
+  p.q = q->data;
+  p.k = k_cache->data;
+  p.v = v_cache->data;
+  p.pos = position->data;
+  p.out = out->data;
+  return QK_OK;
+}
+
+}  // namespace
+
+extern "C" qk_status qk_decode_attention(
+    void* stream, const qk_buffer* q, const qk_buffer* k_cache,
+    const qk_buffer* v_cache, const qk_buffer* position, qk_buffer* out,
+    const qk_attention_attrs* attrs, void* workspace,
+    uint64_t workspace_bytes) {
+  qk::AttentionProblem p;
+  if (qk_status s =
+          CheckAttention(q, k_cache, v_cache, position, out, attrs, &p);
+      s != QK_OK)
+    return s;
+  if (p.b == 0 || p.kv == 0) return QK_OK;
   if (workspace == nullptr || workspace_bytes < p.workspace_bytes) {
     return Fail(QK_INVALID_ARGUMENT,
                 "qkern: decode attention needs a workspace of " +
@@ -1009,11 +1033,6 @@ extern "C" qk_status qk_decode_attention(
     return Fail(QK_INVALID_ARGUMENT,
                 "qkern: decode attention workspace must be 16-byte aligned");
   }
-  p.q = q->data;
-  p.k = k_cache->data;
-  p.v = v_cache->data;
-  p.pos = position->data;
-  p.out = out->data;
   if (qk_status s = qk::PreLaunch(); s != QK_OK) return s;
   return qk::LaunchAttention(p, workspace, static_cast<hipStream_t>(stream));
 }
