@@ -275,6 +275,27 @@ qk_status qk_decode_attention(void* stream, const qk_buffer* q,
                               const qk_attention_attrs* attrs,
                               void* workspace, uint64_t workspace_bytes);
 
+/* qk$decode_attention without a workspace and without any allocation: the
+ * split window's partials go to a fixed device scratch of
+ * QK_ATTENTION_SCRATCH_BYTES that the library holds on each device it runs
+ * on until the process ends. It has no counterpart in the reference; it is
+ * for callers that cannot allocate device memory (HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same operands, checks and
+ * results as qk_decode_attention; shapes whose partials
+ * (qk_decode_attention_workspace_size) exceed the scratch are refused with
+ * QK_INVALID_ARGUMENT. The stream must belong to the current device. Every
+ * call on one device shares that device's scratch: calls that overlap on
+ * one device (different streams, or different threads without ordering)
+ * race and give wrong results. Nothing in the scratch needs clearing: each
+ * call writes every partial it reads. */
+#define QK_ATTENTION_SCRATCH_BYTES (8u << 20)
+qk_status qk_decode_attention_noalloc(void* stream, const qk_buffer* q,
+                                      const qk_buffer* k_cache,
+                                      const qk_buffer* v_cache,
+                                      const qk_buffer* position,
+                                      qk_buffer* out,
+                                      const qk_attention_attrs* attrs);
+
 /* ------------------------------------------------------------------------
  * Status.
  * ---------------------------------------------------------------------- */

@@ -36,6 +36,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 #include "qk_device.h"
@@ -306,6 +307,43 @@ void PlanAttention(AttentionProblem* p) {
   p->parts = static_cast<int>((chunks + cpw - 1) / cpw);
   p->workspace_bytes = static_cast<uint64_t>(bkv) * p->parts * p->g *
                        (p->d + 2) * sizeof(float);
+}
+
+// The fixed scratch of qk_decode_attention_noalloc: the partials of the
+// split window live here instead of in a caller workspace. Each device holds
+// its own copy for the life of the process. Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the
+// symbol); it uses the device address hipGetSymbolAddress returns.
+static __device__ __align__(256) float scratch[kAttentionScratchBytes /
+                                               sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+qk_status AttentionScratch(void** ptr) {
+  *ptr = nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    return Fail(QK_INTERNAL, "qkern: no current HIP device for the "
+                             "attention scratch");
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    // Resolved once per device, with that device current.
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      return Fail(QK_INTERNAL,
+                  std::string("qkern: hipGetSymbolAddress(scratch) failed: ") +
+                      hipGetErrorString(e));
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return QK_OK;
 }
 
 qk_status LaunchAttention(const AttentionProblem& p, void* workspace,

@@ -1037,6 +1037,30 @@ extern "C" qk_status qk_decode_attention(
   return qk::LaunchAttention(p, workspace, static_cast<hipStream_t>(stream));
 }
 
+extern "C" qk_status qk_decode_attention_noalloc(
+    void* stream, const qk_buffer* q, const qk_buffer* k_cache,
+    const qk_buffer* v_cache, const qk_buffer* position, qk_buffer* out,
+    const qk_attention_attrs* attrs) {
+  qk::AttentionProblem p;
+  if (qk_status s =
+          CheckAttention(q, k_cache, v_cache, position, out, attrs, &p);
+      s != QK_OK)
+    return s;
+  if (p.b == 0 || p.kv == 0) return QK_OK;
+  if (p.workspace_bytes > qk::kAttentionScratchBytes) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: decode attention at these shapes needs " +
+                    std::to_string(p.workspace_bytes) +
+                    " bytes of partials, more than the fixed scratch of " +
+                    std::to_string(qk::kAttentionScratchBytes) +
+                    " bytes; call qk_decode_attention with a workspace");
+  }
+  if (qk_status s = qk::PreLaunch(); s != QK_OK) return s;
+  void* scratch = nullptr;
+  if (qk_status s = qk::AttentionScratch(&scratch); s != QK_OK) return s;
+  return qk::LaunchAttention(p, scratch, static_cast<hipStream_t>(stream));
+}
+
 // ---------------------------------------------------------------------------
 // Status entry points.
 

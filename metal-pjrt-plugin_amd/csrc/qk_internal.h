@@ -158,6 +158,16 @@ struct AttentionProblem {
 };
 
 void PlanAttention(AttentionProblem* p);
+
+// Bytes of the fixed device scratch qk_decode_attention_noalloc uses in
+// place of a workspace (one copy per device, held until the process ends).
+constexpr uint64_t kAttentionScratchBytes = uint64_t{8} << 20;
+static_assert(kAttentionScratchBytes == QK_ATTENTION_SCRATCH_BYTES,
+              "the scratch size the header states");
+
+// The current device's address of that scratch (resolved with
+// hipGetSymbolAddress on the first call per device; allocates nothing).
+qk_status AttentionScratch(void** ptr);
 qk_status LaunchAttention(const AttentionProblem& p, void* workspace,
                           hipStream_t stream);
 

@@ -91,6 +91,9 @@ SIGNATURES = {
                                            _P(BufferC), _P(BufferC),
                                            _P(AttentionAttrsC),
                                            ctypes.c_void_p, ctypes.c_uint64]),
+    "qk_decode_attention_noalloc": (ctypes.c_int, [
+        ctypes.c_void_p, _P(BufferC), _P(BufferC), _P(BufferC), _P(BufferC),
+        _P(BufferC), _P(AttentionAttrsC)]),
     "qk_last_error_message": (ctypes.c_char_p, []),
     "qk_device_error": (ctypes.c_int, []),
     "qk_reset_device_error": (None, []),

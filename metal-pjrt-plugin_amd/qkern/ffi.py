@@ -168,3 +168,19 @@ def decode_attention(q, k_cache, v_cache, position, *, scale=None, window=0,
         _ref(bo), ctypes.byref(attrs), workspace.data_ptr(),
         workspace.numel() * workspace.element_size()))
     return out
+
+
+def decode_attention_noalloc(q, k_cache, v_cache, position, *, out,
+                             scale=None, window=0, stream=None):
+    """qk$decode_attention through the entry point that allocates nothing
+    (qk_decode_attention_noalloc): the partials go to the library's fixed
+    per-device scratch. `out` is required (the caller owns every buffer).
+    Calls that overlap on one device race on that scratch."""
+    attrs = _attn_attrs(q, scale, window)
+    pos = position.reshape(1) if position.dim() == 0 else position
+    bq, bk, bv, bp, bo = (any_buffer(t) for t in (q, k_cache, v_cache, pos,
+                                                   out))
+    check(lib().qk_decode_attention_noalloc(
+        stream_handle(stream), _ref(bq), _ref(bk), _ref(bv), _ref(bp),
+        _ref(bo), ctypes.byref(attrs)))
+    return out
