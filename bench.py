@@ -241,6 +241,138 @@ def secondary(torch, qkern, dev, gen):
     return out
 
 
+def secondary_more(torch, qkern, dev, gen):
+    """Few-row dense GEMMs, decode attention and the device copy ceiling."""
+    out = []
+    L = qkern.blas
+    # The reference's few-row list (docs/performance.md:223-242,
+    # examples/llm/skinny_jax.py): 28 GEMMs x[M, 1024] @ W.T, bf16
+    # W [6144, 1024] (28 distinct weights, 352 MB), one call = all 28.
+    nl, kk, nn = 28, 1024, 6144
+    ws = [(0.02 * torch.randn(nn, kk, device=dev, generator=gen)).to(
+        torch.bfloat16) for _ in range(nl)]
+    for m in (1, 2, 4, 8, 16, 32, 64):
+        x = (0.01 * torch.ones(m, kk, device=dev)).to(torch.bfloat16)
+        ys = [torch.empty(m, nn, dtype=torch.bfloat16, device=dev)
+              for _ in range(nl)]
+        plan = L.BlasLt.get_matmul_plan(
+            L.GemmConfig(L.MatrixLayout("bfloat16", m, kk),
+                         L.MatrixLayout("bfloat16", kk, nn,
+                                        L.Order.kColumnMajor, 1, kk, 0),
+                         L.MatrixLayout("bfloat16", m, nn),
+                         L.MatrixLayout("bfloat16", m, nn)),
+            L.Epilogue.kDefault)
+
+        def call(i, x=x, ys=ys, plan=plan):
+            for j in range(nl):
+                plan.execute_on_stream(None, L.MemoryArgs(x, ws[j], None,
+                                                          ys[j]))
+        ms = timed_launches(torch, call, 4)
+        nbytes = nl * (nn * kk * 2 + m * kk * 2 + m * nn * 2)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"name": f"bf16 few-row gemm list 28x[{m},1024]x"
+                            f"[1024,6144]^T", "value": round(gbs, 1),
+                    "unit": "GB/s", "ms": round(ms, 4),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4),
+                    "kernel": plan.describe().split("kernel=")[-1]})
+    del ws
+    # Decode attention at Qwen3-8B's shape (32 query heads over 8 KV heads
+    # of dim 128), one sequence, the whole cache attended: K + V read once
+    for smax in (4096, 32768):
+        b, kv, g, d = 1, 8, 4, 128
+        nset = max(2, -(-(512 << 20) // (2 * b * kv * smax * d * 2)))
+        caches = [(torch.randn(b, kv, smax, d, device=dev, generator=gen).to(
+            torch.bfloat16), torch.randn(b, kv, d, smax, device=dev,
+                                         generator=gen).to(torch.bfloat16))
+            for _ in range(nset)]
+        q = torch.randn(b, kv, g, d, device=dev, generator=gen).to(
+            torch.bfloat16)
+        pos = torch.tensor([smax - 1], dtype=torch.int32, device=dev)
+        o = torch.empty_like(q)
+        wsp = torch.empty(qkern.decode_attention_workspace_size(
+            q, caches[0][0]), dtype=torch.uint8, device=dev)
+        fn = lambda i: qkern.decode_attention(q, *caches[i % nset], pos,
+                                              workspace=wsp, out=o)
+        fn(0)
+        ms = timed_launches(torch, fn, 32)
+        nbytes = 2 * b * kv * smax * d * 2 + 2 * q.numel() * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"name": f"decode attention bf16 B=1 KV=8 G=4 D=128 "
+                            f"S={smax}", "value": round(gbs, 1),
+                    "unit": "GB/s", "ms": round(ms, 4),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del caches
+    # The practical read+write ceiling: a plain device copy of the rownorm
+    # sizes (rotating over 8 sources, 537 MB or more)
+    for mb, dt in ((67, torch.bfloat16), (134, torch.float32)):
+        srcs = [torch.empty(4096, 4096, dtype=dt, device=dev).normal_(
+            generator=gen) for _ in range(8)]
+        dst = torch.empty_like(srcs[0])
+        fn = lambda i: dst.copy_(srcs[i % 8])
+        fn(0)
+        ms = timed_launches(torch, fn, 32)
+        nbytes = 2 * srcs[0].numel() * srcs[0].element_size()
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"name": f"device copy 4096x4096 {str(dt)[6:]} "
+                            f"(read+write {2 * mb} MB)", "value": round(gbs, 1),
+                    "unit": "GB/s", "ms": round(ms, 4),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del srcs
+    return out
+
+
+def cpu_secondary(seconds=3.0):
+    """CPU figures beside the GEMM and rownorm secondaries: torch's CPU
+    backend running the same programs (bf16 GEMM + bias + SiLU at
+    4096^3, f32 GEMM 1024^3, RMSNorm and softmax [4096, 4096]) on the host
+    cores, each repeated for about `seconds`."""
+    import torch
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    res = []
+
+    def rate(fn):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            fn()
+            n += 1
+        return (time.perf_counter() - t0) / n
+
+    a = (torch.randn(4096, 4096, generator=g) / 64).to(torch.bfloat16)
+    b = (torch.randn(4096, 4096, generator=g) / 64).to(torch.bfloat16)
+    bias = (0.02 * torch.randn(4096, generator=g)).to(torch.bfloat16)
+    dt = rate(lambda: torch.nn.functional.silu(
+        (a.float() @ b.float() + bias.float())).to(torch.bfloat16))
+    res.append({"name": "bf16 gemm+bias+silu 4096x4096x4096",
+                "value": round(2 * 4096 ** 3 / dt / 1e12, 3),
+                "unit": "TFLOP/s"})
+    a = torch.randn(1024, 1024, generator=g)
+    b = torch.randn(1024, 1024, generator=g)
+    dt = rate(lambda: a @ b)
+    res.append({"name": "f32 gemm 1024x1024x1024",
+                "value": round(2 * 1024 ** 3 / dt / 1e12, 3),
+                "unit": "TFLOP/s"})
+    x = torch.randn(4096, 4096, generator=g)
+    w = 1 + 0.1 * torch.randn(4096, generator=g)
+    xb = x.to(torch.bfloat16)
+    dt = rate(lambda: (xb.float() * torch.rsqrt(
+        xb.float().pow(2).mean(-1, keepdim=True) + 1e-6) * w).to(
+            torch.bfloat16))
+    res.append({"name": "rmsnorm bf16 4096x4096",
+                "value": round(2 * 4096 * 4096 * 2 / dt / 1e9, 2),
+                "unit": "GB/s"})
+    dt = rate(lambda: torch.softmax(x, -1))
+    res.append({"name": "softmax f32 4096x4096",
+                "value": round(2 * 4096 * 4096 * 4 / dt / 1e9, 2),
+                "unit": "GB/s"})
+    return {"impl": "torch CPU (float32 arithmetic, bf16 rounding of the "
+                    "output), in place of JAX_PLATFORMS=cpu: jax is not "
+                    "installed", "cores": threads, "kind": "port",
+            "results": res}
+
+
 def cpu_baseline(seconds=12.0):
     """The oracle's C port of _matvec_int4 on a bounded sample: repeated
     passes over the four Qwen3-8B shapes (M = 1) until `seconds` elapse."""
@@ -389,9 +521,12 @@ def main():
                                "timed step)"},
     }
     if not args.no_secondary:
-        result["secondary"] = secondary(torch, qkern, dev, gen)
+        result["secondary"] = (secondary(torch, qkern, dev, gen) +
+                               secondary_more(torch, qkern, dev, gen))
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
+        if not args.no_secondary:
+            result["cpu_secondary"] = cpu_secondary()
     print(json.dumps(result), flush=True)
 
 
