@@ -262,10 +262,12 @@ qk_status qk_decode_attention_workspace_size(const qk_buffer* q,
  *   t[s] = scale * sum_d q[d] k[s, d] for slots s < window with s <= pos,
  *   p = softmax(t), out[g, d] = sum_s p[s] v[d, s]
  * in f32, rounded once into out (q's shape and type). q, caches and out
- * are all bf16 or all f16; D is 64 or 128; G <= 16; Smax a multiple of 8;
- * buffers 16-byte aligned. The position is read on the device (a jitted
- * decode loop passes it as a traced value); slots past min(window, pos + 1)
- * are not read. `workspace` (device memory of at least
+ * are all bf16 or all f16; D is 64 or 128; G <= 16; Smax a multiple of 8
+ * and at most 2^22; buffers 16-byte aligned. The position is read on the
+ * device (a jitted decode loop passes it as a traced value); slots past
+ * min(window, pos + 1) take no part, whatever they hold (keys there are
+ * not read; values are read in 8-slot units, units wholly past it are
+ * not). `workspace` (device memory of at least
  * qk_decode_attention_workspace_size bytes, contents ignored, clobbered)
  * holds the partials of the split window. */
 qk_status qk_decode_attention(void* stream, const qk_buffer* q,

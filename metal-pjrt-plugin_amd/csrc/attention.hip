@@ -13,24 +13,28 @@
 // init_cache (qwen3.py:279-291): keys [B, KV, Smax, D], values
 // [B, KV, D, Smax], each with the reduced axis last.
 //
-// attn_split_kernel: one wavefront per (b, h, run of cpw 64-slot chunks).
-// Scores come from v_mfma_f32_16x16x32 with the query heads as the 16 rows
-// (heads past G are zero rows) and 16 slots as columns: lane l reads the 16
-// contiguous bytes of key row (slot) l % 16 at head-dim offset 8 (l / 16)
-// of each 32-wide step, so a wave instruction covers whole 256-byte key
-// rows. The chunk's softmax is folded into a running maximum, sum and
-// accumulator (exponentials as exp2 of log2(e)-scaled scores). p goes
-// through a wave-private LDS tile into the A operand of a second MFMA
-// whose B operand reads 16 contiguous bytes of value row d (8 slots): p is
-// split exactly into two bf16 (or f16) parts, hi + lo, so p.v keeps ~2^-17
-// relative precision, as f32 arithmetic would. Each wave writes its
-// partial (max, sum, accumulator row per head) to the workspace.
-// attn_combine_kernel: one wavefront per (b, h, g) rescales the partials
-// to the common maximum and divides by the total sum.
+// attn_split_kernel: one wavefront per (b, h, run of 64-slot chunks); the
+// runs cut the attended window (known only on the device) into a fixed
+// number of parts. Keys and values of a chunk are fetched by LDS DMA as
+// whole contiguous 1 KB pieces into one of two LDS stages (the next chunk
+// is in flight while one is computed) and read back, swizzled against
+// bank conflicts, in the MFMA operand layouts. Scores come from
+// v_mfma_f32_16x16x32 with the query heads as the 16 rows (heads past G
+// are zero rows) and 16 slots as columns. The chunk's softmax is folded
+// into a running maximum, sum and accumulator (exponentials as exp2 of
+// log2(e)-scaled scores). p goes through a wave-private LDS tile into the
+// A operand of a second MFMA whose B operand is 8 slots of a value row:
+// p is split exactly into two bf16 (or f16) parts, hi + lo, so p.v keeps
+// ~2^-17 relative precision, as f32 arithmetic would. Each wave writes
+// its partial (max, sum, accumulator row per head) to the workspace.
+// attn_combine_kernel: one workgroup per (b, h, g) and 16 head-dim
+// columns rescales the partials to the common maximum and divides by the
+// total sum.
 //
-// Slots past min(window, pos + 1) are never read: the loads use buffer
-// descriptors whose extent ends there (or an out-of-range offset), which
-// return zeros without touching memory, and their scores are -inf.
+// Slots past min(window, pos + 1) take no part: keys past it read zeros
+// through the descriptor's extent and score -inf; values are fetched in
+// 8-slot units, units wholly past it are not read, and the slots past it
+// in the last unit are zeroed in LDS before use.
 
 #include <hip/hip_runtime.h>
 
@@ -63,15 +67,17 @@ struct AttnArgs {
   void* out;         // [B, KV, G, D]
   float* part;       // [B*KV][parts][G][D]
   float* ml;         // [B*KV][parts][G][2]: running max (log2 units), sum
-  int g, smax, window, parts, cpw;
+  int g, smax, window, parts;
   float scale_log2;  // scale * log2(e)
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t Rsrc(const void* p,
-                                                       long long bytes) {
-  const int b = static_cast<int>(std::min<long long>(bytes, 0x7FFFFFFFll));
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, b,
-                                           0x00020000);
+// The attended window is split into `parts` runs of whole chunks per
+// (b, h); both kernels derive the run length from the position read on the
+// device, so a short attended prefix of a long window still spreads over
+// all parts.
+__device__ __forceinline__ int ChunksPerPart(int valid, int parts) {
+  const int cv = (valid + kChunk - 1) / kChunk;
+  return (cv + parts - 1) / parts;
 }
 
 template <typename T>
@@ -103,69 +109,129 @@ __device__ __forceinline__ float sum16(float v) {
   return v;
 }
 
+// LDS of one split wave: two stages of a chunk's keys and values, the q
+// tile and the p tile. Keys land as their 64 rows of D/8 16-byte units,
+// unit c of slot s at position c ^ Swz(s); values as D rows of 8 units
+// (64 slots), unit u of row d at u ^ ((d >> 1) & 7). Both swizzles make
+// the MFMA operand reads (16 lanes: 16 slots, or 16 rows, at one unit)
+// hit 16 distinct 16-byte bank groups.
+template <int D>
+struct AttnLds {
+  static constexpr int kUnits = D / 8;
+  static constexpr int kK = kChunk * D * 2;
+  static constexpr int kV = D * kChunk * 2;
+  static constexpr int kStage = kK + kV;
+  static constexpr int kDmaK = kK / 1024;  // 1 KB DMA instructions
+  static constexpr int kDmaV = kV / 1024;
+  static constexpr int kDma = kDmaK + kDmaV;
+  static constexpr int kQ = 16 * D * 2;
+  static constexpr int kQOff = 2 * kStage;
+  static constexpr int kPOff = kQOff + kQ;
+  static constexpr int kBytes = kPOff + 16 * kPStride * 4;
+  static __device__ __forceinline__ int Swz(int s) {
+    return D == 128 ? (s & 15) : ((s >> 1) & 7);
+  }
+};
+
 template <typename T, int D>
 __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
   using M = Mfma<T>;
   using V = typename M::V;
+  using L = AttnLds<D>;
   constexpr int kSteps = D / 32;  // 32-wide head-dim steps of a score MFMA
   constexpr int kDB = D / 16;     // 16-wide head-dim blocks of the output
-  __shared__ __attribute__((aligned(16))) float ptile[16 * kPStride];
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  float* ptile = reinterpret_cast<float*>(smem + L::kPOff);
 
   const int lane = threadIdx.x;
   const int bh = blockIdx.y;
   const int w = blockIdx.x;
   const int pos = __builtin_amdgcn_readfirstlane(*a.pos);
   const int valid = min(a.window, pos + 1);  // slots [0, valid) attended
-  const int s_begin = w * a.cpw * kChunk;
+  const int cpw = ChunksPerPart(valid, a.parts);
+  const int s_begin = w * cpw * kChunk;
   if (s_begin >= valid) return;  // the combine reads only partials below
-  const int s_end = min(valid, s_begin + a.cpw * kChunk);
+  const int s_end = min(valid, s_begin + cpw * kChunk);
+  const int nchunks = (s_end - s_begin + kChunk - 1) / kChunk;
+
+  const T* qb = static_cast<const T*>(a.q) + static_cast<long long>(bh) * a.g * D;
+  const T* kb = static_cast<const T*>(a.k) + static_cast<long long>(bh) * a.smax * D;
+  const T* vb = static_cast<const T*>(a.v) + static_cast<long long>(bh) * D * a.smax;
+  // Keys up to the last attended slot (rows past it read zeros); values
+  // of this (b, h) (8-slot units wholly past it are not read).
+  DmaRsrc qd, kd, vd;
+  qd.make(qb, static_cast<long long>(a.g) * D * 2);
+  kd.make(kb, static_cast<long long>(valid) * D * 2);
+  vd.make(vb, static_cast<long long>(D) * a.smax * 2);
+
+  // Per-lane DMA offsets within a chunk: key unit p = 64 i + lane is slot
+  // p / kUnits, unit (p % kUnits) ^ Swz(slot); value lane covers row
+  // 8 i + lane / 8, unit (lane % 8) ^ ((row >> 1) & 7).
+  auto issue = [&](int chunk) {
+    unsigned char* st = smem + (chunk & 1) * L::kStage;
+    const int s0 = s_begin + chunk * kChunk;
+#pragma unroll
+    for (int i = 0; i < L::kDmaK; ++i) {
+      const int p = 64 * i + lane;
+      const int sl = p / L::kUnits;
+      const int u = (p % L::kUnits) ^ L::Swz(sl);
+      kd.dma(st + 1024 * i, ((s0 + sl) * L::kUnits + u) * 16, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < L::kDmaV; ++i) {
+      const int d = 8 * i + lane / 8;
+      const int u = (lane % 8) ^ ((d >> 1) & 7);
+      const int sv = s0 + 8 * u;
+      vd.dma(st + L::kK + 1024 * i, sv < valid ? (d * a.smax + sv) * 2 : kOut,
+             0);
+    }
+  };
+
+  // q first (heads past G read zeros), then the first two chunks.
+#pragma unroll
+  for (int i = 0; i < (L::kQ + 1023) / 1024; ++i)
+    qd.dma(smem + L::kQOff + 1024 * i, (1024 * i + 16 * lane), 0);
+  issue(0);
+  if (nchunks > 1) issue(1);
 
   const int r16 = lane & 15, q4 = lane >> 4;
-  // q as the A operand: row r16 = head (zero past G), K = head-dim
-  // 32 t + 8 q4 .. + 7.
-  const auto qrs = Rsrc(static_cast<const T*>(a.q) +
-                            static_cast<long long>(bh) * a.g * D,
-                        static_cast<long long>(a.g) * D * 2);
-  V qf[kSteps];
-#pragma unroll
-  for (int t = 0; t < kSteps; ++t) {
-    const int off = r16 < a.g ? (r16 * D + 32 * t + 8 * q4) * 2 : kOut;
-    qf[t] = __builtin_bit_cast(
-        V, __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, 0));
-  }
-  // keys of this (b, h) up to the last attended slot; values per row d
-  const auto krs = Rsrc(static_cast<const T*>(a.k) +
-                            static_cast<long long>(bh) * a.smax * D,
-                        static_cast<long long>(valid) * D * 2);
-  const auto vrs = Rsrc(static_cast<const T*>(a.v) +
-                            static_cast<long long>(bh) * D * a.smax,
-                        static_cast<long long>(D) * a.smax * 2);
-
   float m_run[4], l_run[4];
   f32x4 acc[kDB];
 #pragma unroll
   for (int r = 0; r < 4; ++r) m_run[r] = -__builtin_inff(), l_run[r] = 0.f;
 #pragma unroll
   for (int db = 0; db < kDB; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  V qf[kSteps];
 
-  for (int s0 = s_begin; s0 < s_end; s0 += kChunk) {
-    // Loads of the whole chunk first: keys (4 blocks of 16 slots x
-    // kSteps), values (2 steps of 32 slots x kDB blocks of 16 rows).
-    u32x4 kr[4][kSteps], vr[2][kDB];
+  for (int c = 0; c < nchunks; ++c) {
+    if (c + 1 < nchunks)
+      __builtin_amdgcn_s_waitcnt(VmcntImm(L::kDma));  // chunk c landed
+    else
+      __builtin_amdgcn_s_waitcnt(VmcntImm(0));
+    const unsigned char* st = smem + (c & 1) * L::kStage;
+    const int s0 = s_begin + c * kChunk;
+    if (c == 0) {
+      // q as the A operand: row r16 = head (zero past G), K = head-dim
+      // 32 t + 8 q4 .. + 7.
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+      for (int t = 0; t < kSteps; ++t) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(
+            smem + L::kQOff + (r16 * D + 32 * t + 8 * q4) * 2);
+        qf[t] = __builtin_bit_cast(V, r16 < a.g ? v : u32x4{0, 0, 0, 0});
+      }
+    }
+    // The values of slots [valid, next multiple of 8) were fetched with
+    // their unit: zero them (a value there may be anything, even NaN, and
+    // p = 0 would not cancel it).
+    if (valid - s0 < kChunk && (valid & 7) != 0) {
+      const int su = (valid - s0) >> 3;  // unit holding slot valid
+      unsigned char* vs = const_cast<unsigned char*>(st) + L::kK;
 #pragma unroll
-      for (int t = 0; t < kSteps; ++t)
-        kr[j][t] = __builtin_amdgcn_raw_buffer_load_b128(
-            krs, ((s0 + 16 * j + r16) * D + 32 * t + 8 * q4) * 2, 0, 0);
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int sv = s0 + 32 * u + 8 * q4;  // first of the lane's 8 slots
-#pragma unroll
-      for (int db = 0; db < kDB; ++db) {
-        const int off =
-            sv < valid ? ((16 * db + r16) * a.smax + sv) * 2 : kOut;
-        vr[u][db] = __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0);
+      for (int rr = 0; rr < D / 64; ++rr) {
+        const int d = 64 * rr + lane;
+        T* row = reinterpret_cast<T*>(vs + d * 128 +
+                                      (su ^ ((d >> 1) & 7)) * 16);
+        for (int e = valid & 7; e < 8; ++e) row[e] = from_f32<T>(0.f);
       }
     }
     // Scores: lane l holds heads 4 q4 + r for slot s0 + 16 j + r16.
@@ -173,10 +239,14 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       sc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int sl = 16 * j + r16;
 #pragma unroll
-      for (int t = 0; t < kSteps; ++t)
-        sc[j] = M::run(qf[t], __builtin_bit_cast(V, kr[j][t]), sc[j]);
-      const bool in = s0 + 16 * j + r16 < valid;
+      for (int t = 0; t < kSteps; ++t) {
+        const u32x4 kv = *reinterpret_cast<const u32x4*>(
+            st + (sl * L::kUnits + ((4 * t + q4) ^ L::Swz(sl))) * 16);
+        sc[j] = M::run(qf[t], __builtin_bit_cast(V, kv), sc[j]);
+      }
+      const bool in = s0 + sl < valid;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         sc[j][r] = in ? sc[j][r] * a.scale_log2 : -__builtin_inff();
@@ -226,12 +296,18 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
       }
 #pragma unroll
       for (int db = 0; db < kDB; ++db) {
-        const V vb = __builtin_bit_cast(V, vr[u][db]);
-        acc[db] = M::run(hi, vb, acc[db]);
-        acc[db] = M::run(lo, vb, acc[db]);
+        const int d = 16 * db + r16;
+        const u32x4 vv = *reinterpret_cast<const u32x4*>(
+            st + L::kK + d * 128 + ((4 * u + q4) ^ ((d >> 1) & 7)) * 16);
+        const V vbf = __builtin_bit_cast(V, vv);
+        acc[db] = M::run(hi, vbf, acc[db]);
+        acc[db] = M::run(lo, vbf, acc[db]);
       }
     }
-    __builtin_amdgcn_wave_barrier();  // the tile's reads before next writes
+    // This stage's LDS reads are done before its refill is issued.
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    if (c + 2 < nchunks) issue(c + 2);
   }
 
   // Partial of this wave: heads 4 q4 + r < G.
@@ -252,59 +328,106 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
   }
 }
 
-// One wavefront per (b, h, g): o = sum_c 2^(m_c - M) acc_c /
-// sum_c 2^(m_c - M) l_c over the partials that hold attended slots.
+// One workgroup of 256 threads per (b, h, g) and 16 head-dim columns:
+// o = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c over the partials
+// that hold attended slots. Thread t takes column t % 16 of partials
+// c = t / 16, t / 16 + 16, ... (16 partial rows in flight per workgroup,
+// 64 contiguous bytes each); the 16 sums per column meet in LDS.
+constexpr int kCombineThreads = 256;
+constexpr int kCombineCols = 16;
+constexpr int kCombineGroups = kCombineThreads / kCombineCols;
+
 template <typename T, int D>
-__global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
-  const int lane = threadIdx.x;
+__global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(
+    AttnArgs a) {
+  __shared__ float red[kCombineGroups][kCombineCols + 1];
+  __shared__ float dred[kCombineGroups];
+  __shared__ float wmax[kCombineThreads / 64];
+  const int t = threadIdx.x;
   const int bhg = blockIdx.x;  // (b * KV + h) * G + g
   const int bh = bhg / a.g, g = bhg % a.g;
+  const int col = blockIdx.y * kCombineCols + (t % kCombineCols);
+  const int cg = t / kCombineCols;
+  const float* ml = a.ml + static_cast<long long>(bh) * a.parts * a.g * 2;
+  const float* part = a.part + static_cast<long long>(bh) * a.parts * a.g * D;
+  // The first kFirst partials of this thread are requested before the
+  // position arrives (those past the attended ones are loaded, never
+  // used), so the kernel waits for one memory round trip, not three.
+  constexpr int kFirst = 8;
+  float pm[kFirst], pl[kFirst], pp[kFirst];
+#pragma unroll
+  for (int i = 0; i < kFirst; ++i) {
+    const int c = cg + kCombineGroups * i;
+    const bool ok = c < a.parts;
+    const long long e = static_cast<long long>(ok ? c : 0) * a.g + g;
+    pm[i] = ml[e * 2];
+    pl[i] = ml[e * 2 + 1];
+    pp[i] = part[e * D + col];
+  }
   const int pos = __builtin_amdgcn_readfirstlane(*a.pos);
   const int valid = min(a.window, pos + 1);
-  const int span = a.cpw * kChunk;
+  const int span = ChunksPerPart(valid, a.parts) * kChunk;
   const int np = valid <= 0 ? 0 : min(a.parts, (valid + span - 1) / span);
-  const float* ml = a.ml + static_cast<long long>(bh) * a.parts * a.g * 2;
   float mx = -__builtin_inff();
-  for (int c = lane; c < np; c += 64) mx = fmaxf(mx, ml[(c * a.g + g) * 2]);
-  mx = wave_max(mx);
-  constexpr int kPer = D / 64;
-  float num[kPer], den = 0.f;
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) num[i] = 0.f;
-  const float* part = a.part + static_cast<long long>(bh) * a.parts * a.g * D;
-  for (int c = 0; c < np; ++c) {
+  for (int i = 0; i < kFirst; ++i)
+    if (cg + kCombineGroups * i < np) mx = fmaxf(mx, pm[i]);
+  for (int c = cg + kCombineGroups * kFirst; c < np; c += kCombineGroups)
+    mx = fmaxf(mx, ml[(c * a.g + g) * 2]);
+  mx = wave_max(mx);
+  if ((t & 63) == 0) wmax[t >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  float num = 0.f, den = 0.f;
+#pragma unroll
+  for (int i = 0; i < kFirst; ++i) {
+    if (cg + kCombineGroups * i < np) {
+      const float wgt = __builtin_amdgcn_exp2f(pm[i] - mx);
+      den += wgt * pl[i];
+      num += wgt * pp[i];
+    }
+  }
+#pragma unroll 4
+  for (int c = cg + kCombineGroups * kFirst; c < np; c += kCombineGroups) {
     const float wgt = __builtin_amdgcn_exp2f(ml[(c * a.g + g) * 2] - mx);
     den += wgt * ml[(c * a.g + g) * 2 + 1];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i)
-      num[i] += wgt * part[(static_cast<long long>(c) * a.g + g) * D +
-                           64 * i + lane];
+    num += wgt * part[(static_cast<long long>(c) * a.g + g) * D + col];
   }
-  // no attended slot: 0 / 0 = NaN, as a softmax over only -inf gives
-  T* o = static_cast<T*>(a.out) + static_cast<long long>(bhg) * D;
+  red[cg][t % kCombineCols] = num;
+  if (t % kCombineCols == 0) dred[cg] = den;
+  __syncthreads();
+  if (cg == 0) {
+    float n = 0.f, dsum = 0.f;
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) o[64 * i + lane] = from_f32<T>(num[i] / den);
+    for (int i = 0; i < kCombineGroups; ++i) {
+      n += red[i][t];
+      dsum += dred[i];
+    }
+    // no attended slot: 0 / 0 = NaN, as a softmax over only -inf gives
+    T* o = static_cast<T*>(a.out) + static_cast<long long>(bhg) * D;
+    o[col] = from_f32<T>(n / dsum);
+  }
 }
 
 template <typename T, int D>
 qk_status Launch(const AttnArgs& a, int bkv, hipStream_t st) {
-  attn_split_kernel<T, D><<<dim3(a.parts, bkv), 64, 0, st>>>(a);
+  attn_split_kernel<T, D><<<dim3(a.parts, bkv), 64, AttnLds<D>::kBytes, st>>>(a);
   if (qk_status s = PostLaunch("attn_split_kernel"); s != QK_OK) return s;
-  attn_combine_kernel<T, D><<<dim3(bkv * a.g), 64, 0, st>>>(a);
+  attn_combine_kernel<T, D>
+      <<<dim3(bkv * a.g, D / kCombineCols), kCombineThreads, 0, st>>>(a);
   return PostLaunch("attn_combine_kernel");
 }
 
 }  // namespace
 
 void PlanAttention(AttentionProblem* p) {
-  // Runs of cpw chunks per wave: one chunk each while that keeps the waves
-  // under ~2048 (8 per CU), longer runs beyond (fewer partials to combine).
+  // About 512 split waves in all (two per CU at head dim 128: each holds
+  // two 32 KB stages of keys and values in LDS): the attended window of
+  // each (b, h) is cut into `parts` runs of whole chunks.
   const int64_t chunks = (p->window + kChunk - 1) / kChunk;
   const int64_t bkv = p->b * p->kv;
-  int64_t cpw = 1;
-  while (bkv * ((chunks + cpw - 1) / cpw) > 2048 && cpw < chunks) cpw *= 2;
-  p->cpw = static_cast<int>(cpw);
-  p->parts = static_cast<int>((chunks + cpw - 1) / cpw);
+  p->parts = static_cast<int>(
+      std::max<int64_t>(1, std::min<int64_t>(chunks, (512 + bkv - 1) / bkv)));
   p->workspace_bytes = static_cast<uint64_t>(bkv) * p->parts * p->g *
                        (p->d + 2) * sizeof(float);
 }
@@ -361,7 +484,6 @@ qk_status LaunchAttention(const AttentionProblem& p, void* workspace,
   a.smax = static_cast<int>(p.smax);
   a.window = static_cast<int>(p.window);
   a.parts = p.parts;
-  a.cpw = p.cpw;
   a.scale_log2 = p.scale * kLog2e;
   if (bkv > 65535) {
     return Fail(QK_UNIMPLEMENTED, "qkern: decode attention over " +

@@ -169,10 +169,6 @@ struct DmaMN192 {
   }
 };
 
-// s_waitcnt immediate for vmcnt(n) (expcnt, lgkmcnt not waited).
-constexpr int VmcntImm(int n) {
-  return (n & 0xF) | (((n >> 4) & 3) << 14) | (7 << 4) | (0xF << 8);
-}
 
 // MC: M need not be a multiple of 256. The A tile's DMA offsets go wholly
 // in the range-checked vector offset (rows, or M-contiguous columns, past

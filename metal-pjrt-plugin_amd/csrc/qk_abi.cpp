@@ -915,10 +915,10 @@ qk_status CheckAttentionShapes(const qk_buffer* q, const qk_buffer* k,
                     BufferString(*k));
   }
   p->smax = k->dims[2];
-  if (p->smax % 8 != 0 || p->smax > (int64_t{1} << 24)) {
+  if (p->smax % 8 != 0 || p->smax > (int64_t{1} << 22)) {
     return Fail(QK_UNIMPLEMENTED,
                 "qkern: decode attention needs a cache length that is a "
-                "multiple of 8 and at most 2^24, got " +
+                "multiple of 8 and at most 2^22, got " +
                     std::to_string(p->smax));
   }
   const int64_t window = attrs->window == 0 ? p->smax : attrs->window;

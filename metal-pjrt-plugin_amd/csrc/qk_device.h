@@ -176,6 +176,11 @@ __device__ __forceinline__ void DmaLds4(__amdgpu_buffer_rsrc_t r,
                                            0);
 }
 
+// s_waitcnt immediate for vmcnt(n) (expcnt, lgkmcnt not waited).
+constexpr int VmcntImm(int n) {
+  return (n & 0xF) | (((n >> 4) & 3) << 14) | (7 << 4) | (0xF << 8);
+}
+
 // Raw buffer descriptor in SGPRs (base, extent in bytes, raw access) whose
 // LDS DMA is issued as inline asm: the compiler's wait-count pass does not
 // see it, so it adds no waits of its own for it (it would otherwise make

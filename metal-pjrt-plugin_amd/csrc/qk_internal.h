@@ -151,9 +151,9 @@ struct AttentionProblem {
   const void* v = nullptr;  // [b, kv, d, smax]
   const void* pos = nullptr;  // int32 device scalar
   void* out = nullptr;        // [b, kv, g, d]
-  // Set by PlanAttention: chunks of 64 slots per wave, partials per (b, kv)
-  // and the workspace they take.
-  int cpw = 1, parts = 0;
+  // Set by PlanAttention: partials per (b, kv) (runs of 64-slot chunks of
+  // the attended window) and the workspace they take.
+  int parts = 0;
   uint64_t workspace_bytes = 0;
 };
 

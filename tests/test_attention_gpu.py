@@ -94,6 +94,29 @@ def test_decode_attention_qwen3_8b(dev, smax, pos, b):
     check_attention(got, q, k, v, pos, 128 ** -0.5, 0)
 
 
+def test_decode_attention_short_prefix_of_long_window(dev):
+    # the window's parts are cut from the position read on the device: a
+    # short attended prefix of a 32768-slot cache still splits over them
+    rng = np.random.default_rng(9)
+    q, k, v = make_case(rng, 1, 8, 4, 128, 32768, "bfloat16")
+    for pos in (0, 100, 4095, 20001):
+        got = run(dev, q, k, v, pos, "bfloat16")
+        check_attention(got, q, k, v, pos, 128 ** -0.5, 0)
+
+
+@pytest.mark.parametrize("pos", [500, 503, 511])
+def test_decode_attention_slots_past_position_take_no_part(dev, pos):
+    # NaN keys and values in every slot past the position (also inside the
+    # last 8-slot unit the values are fetched in) leave the output finite
+    rng = np.random.default_rng(10 + pos)
+    q, k, v = make_case(rng, 2, 2, 4, 128, 1024, "bfloat16")
+    kp, vp = k.copy(), v.copy()
+    kp[:, :, pos + 1:] = np.nan
+    vp[..., pos + 1:] = np.nan
+    got = run(dev, q, kp, vp, pos, "bfloat16")
+    check_attention(got, q, k, v, pos, 128 ** -0.5, 0)
+
+
 def test_decode_attention_peaked_scores(dev):
     # scores up to ~1e3 (unscaled keys far larger than the queries): the
     # running maximum must keep the exponentials finite

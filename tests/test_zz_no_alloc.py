@@ -52,10 +52,11 @@ def test_noalloc_position_on_device_and_window(dev):
 
 
 def test_noalloc_refuses_shapes_past_the_scratch(dev):
-    # 64 KV heads x 16 query heads x 16 chunks of partials: 8.5 MB > 8 MiB
-    q = torch.zeros(1, 64, 16, 128, dtype=torch.bfloat16, device=dev)
-    k = torch.zeros(1, 64, 1024, 128, dtype=torch.bfloat16, device=dev)
-    v = torch.zeros(1, 64, 128, 1024, dtype=torch.bfloat16, device=dev)
+    # 1024 (batch, KV head) pairs x 16 query heads, one partial each:
+    # 8.5 MB > 8 MiB
+    q = torch.zeros(16, 64, 16, 128, dtype=torch.bfloat16, device=dev)
+    k = torch.zeros(16, 64, 64, 128, dtype=torch.bfloat16, device=dev)
+    v = torch.zeros(16, 64, 128, 64, dtype=torch.bfloat16, device=dev)
     pos = torch.zeros(1, dtype=torch.int32, device=dev)
     assert qkern.decode_attention_workspace_size(q, k) > 8 << 20
     with pytest.raises(qkern.QkError) as e:
