@@ -110,6 +110,42 @@ def timed_launches(torch, fn, iters):
     return e0.elapsed_time(e1) / iters
 
 
+def gemm_vs_library(torch, ours, library, iters=20, reps=4, warm_s=0.25):
+    """Median ms per launch of `ours` (graph-replayed, as timed_launches)
+    and of `library` (eager: library calls may record memsets, so they are
+    kept out of graphs), timed in alternating blocks after `warm_s` seconds
+    of `ours`: the clocks of a long GEMM settle with the power draw, so
+    both are timed in the same, settled state, and neither always first."""
+    g = capture(torch, ours, iters)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < warm_s:
+        g.replay()
+        torch.cuda.synchronize()
+
+    def block(fn):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters
+
+    def lib_block():
+        for _ in range(iters):
+            library()
+    mine, lib = [], []
+    for rep in range(reps):
+        if rep % 2 == 0:
+            mine.append(block(g.replay))
+            lib.append(block(lib_block))
+        else:
+            lib.append(block(lib_block))
+            mine.append(block(g.replay))
+    return sorted(mine)[reps // 2], sorted(lib)[reps // 2]
+
+
 def secondary(torch, qkern, dev, gen):
     out = []
     # bf16 GEMM + bias + SiLU (C3), NN row-major: D = silu(A @ B + bias)
@@ -130,23 +166,12 @@ def secondary(torch, qkern, dev, gen):
         args = L.MemoryArgs(a, b, None, d, bias)
         for _ in range(3):
             plan.execute_on_stream(None, args)
-        ms = timed_launches(torch, lambda i: plan.execute_on_stream(None, args),
-                            20)
+        # hipBLASLt (torch.matmul, no epilogue) on the same operands, timed
+        # alternately with it
+        ms, ms_lt = gemm_vs_library(
+            torch, lambda i: plan.execute_on_stream(None, args),
+            lambda: torch.matmul(a, b, out=d))
         tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        # hipBLASLt (torch.matmul, no epilogue) on the same operands, for
-        # reference: eager launches between two events (kept out of graph
-        # capture, as library calls may record memsets)
-        for _ in range(3):
-            torch.matmul(a, b, out=d)
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(20):
-            torch.matmul(a, b, out=d)
-        e1.record()
-        torch.cuda.synchronize()
-        ms_lt = e0.elapsed_time(e1) / 20
         out.append({"name": f"bf16 gemm+bias+silu {m}x{n}x{k}",
                     "value": round(tf, 1), "unit": "TFLOP/s",
                     "ms": round(ms, 4), "frac": round(tf / BF16_PEAK_TFLOPS, 4),

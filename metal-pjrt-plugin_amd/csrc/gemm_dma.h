@@ -12,13 +12,14 @@
 //    conflicts are avoided by choosing which global 16-byte chunk each lane
 //    fetches (an XOR swizzle), not by padding:
 //      K-contiguous operand (A; B stored [N][K]): row r of 128 bytes holds
-//        K chunk c (8 elements) in slot c ^ (r & 7);
+//        K chunk c (8 elements) in slot c ^ ((r >> 1) & 7);
 //      M/N-contiguous operand (B stored [K][N]; A stored [K][M]): K row k
-//        of R elements holds chunk c in slot c ^ 2 (k & 3).
+//        of R elements holds chunk c in slot c ^ 4 (k & 3) (c ^ 2 (k & 3)
+//        for 64-element rows).
 //    K-contiguous fragments are one 16-byte LDS read per lane; the others
 //    are read with the transposing ds_read_b64_tr_b16 (two per fragment).
-//    Both read patterns touch 8 distinct 16-byte slots of one 128-byte
-//    bank row per 8 (16) lanes, i.e. no bank conflicts.
+//    Both read patterns spread each 16-lane group over all 64 banks
+//    (rocprofv3 SQ_LDS_BANK_CONFLICT reads 0 at 4096^3).
 //  - Four waves (2 x 2), each owning 128 x BN/2 of the tile (32x32
 //    blocks, v_mfma_f32_32x32x16_{bf16,f16}), fragments double-buffered in
 //    registers with the LDS reads of K step s + 1 interleaved with the
@@ -43,6 +44,19 @@
 namespace qk {
 namespace {
 
+// Swizzles of the 16-byte chunks of an LDS operand row. K-contiguous
+// rows of 128 bytes (two per 256-byte bank row): chunk c of row r sits in
+// slot c ^ ((r >> 1) & 7), so the 16 rows a 16-lane group reads at one K
+// chunk cover all 64 banks once. M/N-contiguous K rows of 256 bytes or
+// more (LPR >= 16 chunks, every K row on the same banks): chunk c of K row
+// k sits in slot c ^ 4 (k & 3), so the four K rows of a transposing
+// 16-lane read (two chunks each, in 16 chunk slots) meet no bank twice;
+// 128-byte K rows keep c ^ 2 (k & 3) (two K rows per bank row).
+__device__ __forceinline__ constexpr int SwzK(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ constexpr int SwzMN(int k, int lpr) {
+  return lpr >= 16 ? (k & 3) << 2 : (k & 3) << 1;
+}
+
 // Operand tile of R rows x 64 K, K-contiguous in memory (row stride ld
 // elements): R / 32 DMA instructions per wave; instruction i of wave w
 // fills rows (4 i + w) * 8 .. + 8.
@@ -58,7 +72,7 @@ struct DmaK {
                                        int w, int lane) {
     rs.make(src, bytes);
     ld = ld_;
-    voff = ((w * 8 + lane / 8) * ld + ((lane % 8) ^ (lane / 8)) * 8) *
+    voff = ((w * 8 + lane / 8) * ld + ((lane % 8) ^ SwzK(w * 8 + lane / 8)) * 8) *
            static_cast<int>(sizeof(T));
   }
   __device__ __forceinline__ void issue(unsigned char* lds, int r0, int k0,
@@ -76,7 +90,7 @@ struct DmaK {
     const int r = rb + (lane & 31);
     const int c = (kb >> 3) + (lane >> 5);
     return *reinterpret_cast<const typename Frag<T>::type*>(
-        lds + r * 128 + ((c ^ (lane & 7)) << 4));
+        lds + r * 128 + ((c ^ SwzK(r)) << 4));
   }
 };
 
@@ -100,7 +114,7 @@ struct DmaMN {
     ld = ld_;
     const int k = w * RPI + lane / LPR;  // k & 3 is the same for every i
     static_assert((NW * RPI) % 4 == 0, "swizzle phase per instruction");
-    voff = (k * ld + ((lane % LPR) ^ ((k & 3) << 1)) * 8) *
+    voff = (k * ld + ((lane % LPR) ^ SwzMN(k, LPR)) * 8) *
            static_cast<int>(sizeof(T));
   }
   __device__ __forceinline__ void issue(unsigned char* lds, int r0, int k0,
@@ -120,7 +134,7 @@ struct DmaMN {
     const int k = kb + 8 * (g >> 1) + (s >> 2);
     const int n = rb + 16 * (g & 1) + 4 * (s & 3);
     const unsigned char* p =
-        lds + k * RB + (((n >> 3) ^ ((k & 3) << 1)) << 4) + (n & 7) * 2;
+        lds + k * RB + (((n >> 3) ^ SwzMN(k, LPR)) << 4) + (n & 7) * 2;
     const u32x2 lo = lds_read_tr(reinterpret_cast<const T*>(p));
     const u32x2 hi = lds_read_tr(reinterpret_cast<const T*>(p + 4 * RB));
     const u32x4 q = {lo[0], lo[1], hi[0], hi[1]};
@@ -161,7 +175,7 @@ struct DmaMN192 {
     const int k = kb + 8 * (g >> 1) + (s >> 2);
     const int n = (h ? rb - 128 : rb) + 16 * (g & 1) + 4 * (s & 3);
     const unsigned char* p =
-        base + k * RB + (((n >> 3) ^ ((k & 3) << 1)) << 4) + (n & 7) * 2;
+        base + k * RB + (((n >> 3) ^ SwzMN(k, RB / 16)) << 4) + (n & 7) * 2;
     const u32x2 lo2 = lds_read_tr(reinterpret_cast<const T*>(p));
     const u32x2 hi2 = lds_read_tr(reinterpret_cast<const T*>(p + 4 * RB));
     const u32x4 q = {lo2[0], lo2[1], hi2[0], hi2[1]};
