@@ -219,6 +219,8 @@ def test_qmatvec_prefill_tiles(dev, case):
     (1100, 4096, 128, Packing.U8, "bfloat16"),     # 256 x 128, 76-row tail
     (300, 1024, 512, Packing.S8_SYM, "float16"),   # 128 x 128, 44-row tail
     (129, 256, 256, Packing.U32X8, "bfloat16"),    # 128 x 128, one-row tail
+    (300, 12288, 256, Packing.U32X8, "bfloat16"),  # 256 x 96, 44-row tail
+    (700, 384, 512, Packing.U32X8, "float16"),     # 256 x 128 or 96, f16
 ])
 def test_qmatvec_prefill_ragged_rows(dev, case):
     """Row counts that are not multiples of the interior-tile GEMM's tile
