@@ -393,9 +393,9 @@ constexpr HalfTile kHalfTiles[] = {
 };
 constexpr int kFastTile256 = 6, kFastTile128 = 7, kSplitK = 8, kSplitK32 = 9,
               kFastTile192 = 10;
-// f32 problems on the split-bf16 kernel (tile indices below 0: not
-// kHalfTiles entries).
-constexpr int kF32x3Tile128 = -2, kF32x3Tile64 = -3;
+// f32 problems on the split-bf16 kernel, and few-row f16/bf16 problems on
+// the wide gemv (tile indices below 0: not kHalfTiles entries).
+constexpr int kF32x3Tile128 = -2, kF32x3Tile64 = -3, kGemvTile = -4;
 constexpr int kNumHalfTiles = sizeof(kHalfTiles) / sizeof(kHalfTiles[0]);
 
 // Cost of a round of 256x192 interior tiles relative to 256x256.
@@ -488,11 +488,14 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
         if (r < best) best = r, t = c.tile;
       }
     }
+    // At most eight rows of x against NT weights: the wide gemv
+    // (bandwidth-bound on the weights).
+    if (t < 0 && GemvApplies(p)) t = kGemvTile;
     // Few 64x64 tiles and a long K: split K over the waves of each tile
     // (32x32 tiles and eight waves for at most 32 rows or columns).
-    if (t < 0 && tiles(64, 64) < 2 * cus && CeilDiv(p.k, 64) >= 16)
+    if (t == -1 && tiles(64, 64) < 2 * cus && CeilDiv(p.k, 64) >= 16)
       t = std::min(p.m, p.n) <= 32 ? kSplitK32 : kSplitK;
-    if (t < 0) {
+    if (t == -1) {
       // Rounds of resident tiles on the 256 CUs: one 256x256 tile (8
       // waves) per CU, two 128x128 tiles per CU. Measured on MI355X, a
       // round of 128x128 tiles costs ~0.6 of a round of 256x256 tiles.
@@ -505,7 +508,10 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
         t = r256 <= r128 ? 1 : 2;
     }
     c.tile = t;
-    c.bm = kHalfTiles[t].bm, c.bn = kHalfTiles[t].bn, c.bk = 64;
+    if (t == kGemvTile)
+      c.bm = static_cast<int>(p.m), c.bn = 4, c.bk = 512;
+    else
+      c.bm = kHalfTiles[t].bm, c.bn = kHalfTiles[t].bn, c.bk = 64;
   } else {
     // f32: the split-bf16 kernel on interior tiles (128x128 when those
     // fill the GPU, else 64x64), the f32-MFMA tile kernel otherwise.
@@ -538,6 +544,12 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
                              c.tile == kFastTile128);
   const bool splitk = c.tile == kSplitK || c.tile == kSplitK32;
   const bool x3 = c.tile == kF32x3Tile128 || c.tile == kF32x3Tile64;
+  const bool gemv = c.tile == kGemvTile;
+  if (gemv) {
+    c.name = std::string("gemv_nt_") + DTypeName(p.a.dtype) + "_m" +
+             std::to_string(p.m) + "_k" + std::to_string(p.k);
+    return c;
+  }
   c.name = std::string(splitk     ? (c.tile == kSplitK ? "gemm_splitk4_"
                                                        : "gemm_splitk8_")
                        : x3       ? "gemm_f32x3_"
@@ -631,6 +643,7 @@ qk_status LaunchGemm(const GemmProblem& p, hipStream_t stream) {
   const int batch = static_cast<int>(p.batch);
   const bool ta = p.a.transpose, tb = p.b.transpose;
   const char* name = c.name.c_str();
+  if (c.tile == kGemvTile) return LaunchGemv(p, stream);
   switch (p.a.dtype) {
     case QK_BF16:
       return DispatchHalf<bf16>(c.tile, g, batch, ta, tb, stream, name);

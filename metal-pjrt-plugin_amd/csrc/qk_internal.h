@@ -85,6 +85,11 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p);
 // Launches the GEMM. p has been validated; m, n, batch > 0.
 qk_status LaunchGemm(const GemmProblem& p, hipStream_t stream);
 
+// The few-row (M <= 8) f16/bf16 NT kernel (gemv.hip): whether it takes the
+// problem, and its launch.
+bool GemvApplies(const GemmProblem& p);
+qk_status LaunchGemv(const GemmProblem& p, hipStream_t stream);
+
 // ---------------------------------------------------------------------------
 // Quantized matvec / dequantize (qmatvec.hip).
 

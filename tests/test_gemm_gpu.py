@@ -293,6 +293,42 @@ def test_split_k_kernel_few_rows(dev, ta, tb):
     assert "gemm_splitk8" in plan.describe()
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("k", [512, 1024, 2048])
+def test_wide_gemv_few_rows(dev, m, k):
+    """At most eight rows of x against NT weights with K a multiple of 512
+    (the reference's wide gemv: gemv.cc:68-108 takes 2..8 vectors, K >= 512,
+    NT): the bandwidth-bound gemv kernel, with ragged N and both types."""
+    if m * (k // 512) > 16:  # x rows no longer fit the registers
+        plan = run_case(dev, m, 77, k, tb=True)
+        assert "gemv_nt" not in plan.describe()
+        return
+    for n, tin in ((77, "bfloat16"), (1000, "float16"), (6144, "bfloat16")):
+        plan = run_case(dev, m, n, k, tb=True, tin=tin, seed=m * k + n)
+        assert "gemv_nt" in plan.describe(), plan.describe()
+
+
+def test_wide_gemv_epilogues_batches_and_layouts(dev):
+    # every epilogue term, f32 output, alpha / beta with a separate C,
+    # padded leading dimensions, batches with strides and a broadcast B
+    for epi in (Epilogue.kBiasThenSILUWithAux, Epilogue.kBiasThenGELU,
+                Epilogue.kReLU, Epilogue.kBias):
+        plan = run_case(dev, 4, 300, 1024, tb=True, epilogue=epi,
+                        separate_c=True, beta=0.5, alpha=1.5)
+        assert "gemv_nt" in plan.describe()
+    plan = run_case(dev, 8, 129, 512, tb=True, tout="float32", pad=8,
+                    batch=3, beta=1.0)
+    assert "gemv_nt" in plan.describe()
+    plan = run_case(dev, 2, 1000, 2048, tb=True, batch=4, broadcast_b=True,
+                    tin="float16", epilogue=Epilogue.kBiasThenReLU)
+    assert "gemv_nt" in plan.describe()
+    # not NT, or K off the 512 grid: the split-K kernel as before
+    plan = run_case(dev, 4, 700, 1024)
+    assert "gemv_nt" not in plan.describe()
+    plan = run_case(dev, 4, 700, 1000, tb=True)
+    assert "gemv_nt" not in plan.describe()
+
+
 def test_split_k_kernel_epilogues(dev):
     plan = run_case(dev, 32, 1000, 4096, epilogue=Epilogue.kBiasThenSILUWithAux,
                     separate_c=True, beta=1.0)
