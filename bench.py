@@ -327,6 +327,23 @@ def secondary_more(torch, qkern, dev, gen):
                     "unit": "GB/s", "ms": round(ms, 4),
                     "frac": round(gbs / HBM_PEAK_GBS, 4)})
         del caches
+    # Quantized token embedding (qwen3.embed) of Qwen3-8B's int4 table
+    # (151936 x 4096, group 64): 2048 prefill tokens; bytes = the rows'
+    # codes, scales and offsets read and the bf16 rows written
+    n, k = 151936, 4096
+    words, s, b = make_int4(torch, dev, n, k, gen)
+    tok = torch.randint(0, n, (2048,), dtype=torch.int32, device=dev,
+                        generator=gen)
+    rows = torch.empty(2048, k, dtype=torch.bfloat16, device=dev)
+    fn = lambda i: qkern.embed(words, tok, s, b, k=k, out=rows)
+    fn(0)
+    ms = timed_launches(torch, fn, 32)
+    nbytes = 2048 * (k // 2 + (k // GROUP) * 4 + k * 2) + 2048 * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out.append({"name": "int4 embed gather 2048 tokens of 151936x4096",
+                "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
+                "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    del words, s, b, rows
     # The practical read+write ceiling: a plain device copy of the rownorm
     # sizes (rotating over 8 sources, 537 MB or more)
     for mb, dt in ((67, torch.bfloat16), (134, torch.float32)):

@@ -207,6 +207,20 @@ qk_status qk_qmatvec(void* stream, const qk_buffer* x, const qk_buffer* codes,
                      const qk_buffer* scales, const qk_buffer* biases,
                      qk_buffer* y, const qk_quant_attrs* attrs);
 
+/* Target qk$embed: out [tokens..., K] = rows of an embedding table picked
+ * by int32 tokens (any shape; indices outside [0, V) are clamped, as a
+ * JAX gather clamps them). Quantized (scales given): table = codes of
+ * [V, K] in attrs' packing with scales/biases [V, K/g], each picked row
+ * dequantized as qk_dequantize does (f32(q)*f32(s) + f32(b), one rounding
+ * to out's f32, f16 or bf16). Dense (scales NULL): table [V, K] of out's
+ * type, rows copied (16-byte aligned rows). Replaces embed
+ * (examples/llm/qwen3.py:270-274): the gather of q4/q, s, b rows and the
+ * dequantize of qwen3.py:199-207, or w[tokens]. */
+qk_status qk_embed(void* stream, const qk_buffer* tokens,
+                   const qk_buffer* table, const qk_buffer* scales,
+                   const qk_buffer* biases, qk_buffer* out,
+                   const qk_quant_attrs* attrs);
+
 /* Target qk$dequantize: w [N, K] in w's dtype (f32, f16 or bf16), each
  * element computed as f32(q)*f32(scale) + f32(bias) in f32 and rounded once.
  * Replaces dequantize (examples/llm/qwen3.py:199-207). */

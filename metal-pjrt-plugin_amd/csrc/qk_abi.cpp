@@ -791,6 +791,68 @@ extern "C" qk_status qk_dequantize(void* stream, const qk_buffer* codes,
   return qk::LaunchDequantize(q, static_cast<hipStream_t>(stream));
 }
 
+extern "C" qk_status qk_embed(void* stream, const qk_buffer* tokens,
+                              const qk_buffer* table, const qk_buffer* scales,
+                              const qk_buffer* biases, qk_buffer* out,
+                              const qk_quant_attrs* attrs) {
+  if (qk_status s = CheckBuffer(tokens, "tokens", false); s != QK_OK) return s;
+  if (qk_status s = CheckBuffer(table, "table", false); s != QK_OK) return s;
+  if (qk_status s = CheckBuffer(out, "out", false); s != QK_OK) return s;
+  if (tokens->dtype != QK_S32 && tokens->dtype != QK_U32) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: embedding tokens must be int32, got " +
+                    BufferString(*tokens));
+  }
+  // out = tokens' shape + [K]
+  bool shape_ok = out->rank == tokens->rank + 1 && IsFloat(out->dtype);
+  for (int i = 0; shape_ok && i < tokens->rank; ++i)
+    shape_ok = out->dims[i] == tokens->dims[i];
+  if (!shape_ok) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: embedding output must be float [" +
+                    std::string("tokens..., K], got ") + BufferString(*out) +
+                    " for tokens " + BufferString(*tokens));
+  }
+  const int64_t t = NumElements(*tokens);
+  const int64_t k = out->dims[out->rank - 1];
+  if (reinterpret_cast<uintptr_t>(tokens->data) % 4 != 0) {
+    return Fail(QK_INVALID_ARGUMENT, "qkern: tokens must be 4-byte aligned");
+  }
+  if (scales == nullptr) {
+    // A dense table [V, K]: a plain row gather in the table's type.
+    if (table->rank != 2 || table->dtype != out->dtype ||
+        table->dims[1] != k) {
+      return Fail(QK_INVALID_ARGUMENT,
+                  "qkern: dense embedding table must be [V, " +
+                      std::to_string(k) + "] of the output type, got " +
+                      BufferString(*table));
+    }
+    if (t == 0 || k == 0) return QK_OK;
+    if (table->dims[0] == 0) {
+      return Fail(QK_INVALID_ARGUMENT, "qkern: empty embedding table");
+    }
+    if (qk_status s = qk::PreLaunch(); s != QK_OK) return s;
+    return qk::LaunchRowGather(table->data, table->dims[0], k, k,
+                               qk::DTypeSize(out->dtype), tokens->data, t,
+                               out->data, static_cast<hipStream_t>(stream));
+  }
+  qk::QuantProblem q;
+  if (qk_status s = CheckQuant(table, scales, biases, attrs, k, &q);
+      s != QK_OK) {
+    return s;
+  }
+  if (t == 0 || q.k == 0) return QK_OK;
+  if (q.n == 0) {
+    return Fail(QK_INVALID_ARGUMENT, "qkern: empty embedding table");
+  }
+  q.y = out->data;
+  q.y_dtype = out->dtype;
+  q.rows = tokens->data;
+  q.rows_n = t;
+  if (qk_status s = qk::PreLaunch(); s != QK_OK) return s;
+  return qk::LaunchDequantize(q, static_cast<hipStream_t>(stream));
+}
+
 extern "C" qk_status qk_rownorm(void* stream, const qk_buffer* x,
                                 const qk_buffer* gain, const qk_buffer* beta,
                                 qk_buffer* y, const qk_rownorm_attrs* attrs) {

@@ -106,6 +106,10 @@ struct QuantProblem {
   int bias_dtype = QK_BF16;
   void* y = nullptr;  // y dtype == x dtype; for dequantize, the weights
   int y_dtype = QK_BF16;
+  // Embedding gather (qk_embed): output row t is table row rows[t]
+  // (clamped to [0, n)), for t < rows_n; null: every row in order.
+  const void* rows = nullptr;
+  int64_t rows_n = 0;
 };
 
 qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream);
@@ -124,6 +128,12 @@ qk_status LaunchQMid(const QuantProblem& p, hipStream_t stream);
 bool QGemmApplies(const QuantProblem& p);
 qk_status LaunchQGemm(const QuantProblem& p, hipStream_t stream);
 qk_status LaunchDequantize(const QuantProblem& p, hipStream_t stream);
+
+// Dense embedding gather: out[t, :] = table[clamp(rows[t]), :] (k elements
+// of esz bytes per row; table rows ld elements apart).
+qk_status LaunchRowGather(const void* table, int64_t n, int64_t k, int64_t ld,
+                          int esz, const void* rows, int64_t rows_n, void* out,
+                          hipStream_t stream);
 
 // ---------------------------------------------------------------------------
 // Row normalisation (rownorm.hip).

@@ -106,6 +106,8 @@ struct QmvArgs {
   int sdt, bdt;  // scale / bias dtypes (qk_dtype)
   int has_bias;
   int row_bytes;  // bytes of codes per output row
+  const int* gather;  // dequantize: table row of each output row (or null)
+  int out_vec;        // dequantize: 16-byte stores of y allowed
 };
 
 __device__ __forceinline__ uint32_t PackBf16Pair(float lo, float hi) {
@@ -346,45 +348,65 @@ __global__ __launch_bounds__(kWaves * 64) void qmv_generic_kernel(QmvArgs a) {
 // Dequantize: one thread per 16-byte chunk of codes.
 // w = f32(q) * f32(scale) rounded, + f32(bias) rounded, then rounded once
 // more to the output type (no fused multiply-add).
-template <int PACK, typename OT>
+template <int PACK, typename OT, int CPT>
 __global__ void dequant_kernel(QmvArgs a, long long total_chunks) {
-  const long long t = static_cast<long long>(blockIdx.x) * blockDim.x +
-                      threadIdx.x;
-  if (t >= total_chunks) return;
+  // CPT consecutive chunks of one row per thread (one measures faster
+  // than four for a gather of scattered rows).
+  const long long t0 = (static_cast<long long>(blockIdx.x) * blockDim.x +
+                        threadIdx.x) * CPT;
+  if (t0 >= total_chunks) return;
   constexpr bool kInt4 = PACK == QK_PACK_U32X8 || PACK == QK_PACK_BYTE_HALFSPLIT;
   constexpr int kCodes = kInt4 ? 32 : 16;
   const int cpr = a.row_bytes / 16;
-  const int row = static_cast<int>(t / cpr);
-  const int c = static_cast<int>(t % cpr);
+  const int orow = static_cast<int>(t0 / cpr);
+  // An embedding gather reads table row gather[orow], clamped into range
+  // (as a JAX gather clamps out-of-range indices).
+  const int row = a.gather == nullptr
+                      ? orow
+                      : min(max(a.gather[orow], 0), a.n - 1);
+  const int c0 = static_cast<int>(t0 % cpr);
   const int hg = a.group / 2;
-  int kb, grp;
-  if (PACK == QK_PACK_BYTE_HALFSPLIT) {
-    const int byte0 = c * 16;
-    grp = byte0 / hg;
-    kb = grp * a.group + byte0 % hg;
-  } else {
-    kb = c * kCodes;
-    grp = kb / a.group;
+  u32x4 wv[CPT];
+  float sv[CPT], bv[CPT];
+  int kbv[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int c = c0 + j;
+    int kb, grp;
+    if (PACK == QK_PACK_BYTE_HALFSPLIT) {
+      const int byte0 = c * 16;
+      grp = byte0 / hg;
+      kb = grp * a.group + byte0 % hg;
+    } else {
+      kb = c * kCodes;
+      grp = kb / a.group;
+    }
+    kbv[j] = kb;
+    wv[j] = *reinterpret_cast<const u32x4*>(
+        a.codes + static_cast<long long>(row) * a.row_bytes + c * 16);
+    const long long gi = static_cast<long long>(row) * (a.k / a.group) + grp;
+    sv[j] = load_any(a.scales, gi, a.sdt);
+    bv[j] = a.has_bias ? load_any(a.biases, gi, a.bdt) : 0.f;
   }
-  const u32x4 w = *reinterpret_cast<const u32x4*>(
-      a.codes + static_cast<long long>(row) * a.row_bytes + c * 16);
-  const long long gi = static_cast<long long>(row) * (a.k / a.group) + grp;
-  const float s = load_any(a.scales, gi, a.sdt);
-  const float b = a.has_bias ? load_any(a.biases, gi, a.bdt) : 0.f;
-  OT* out = static_cast<OT*>(a.y) + static_cast<long long>(row) * a.k + kb;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+  const u32x4 w = wv[j];
+  const float s = sv[j], b = bv[j];
+  OT* out = static_cast<OT*>(a.y) + static_cast<long long>(orow) * a.k + kbv[j];
+  // The chunk's values by output offset from kb: 32 (int4) or 16 (int8)
+  // consecutive elements; half-split int4: 16 at 0 and 16 at hg.
+  float v[kCodes];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t word = w[i];
     if (kInt4) {
 #pragma unroll
       for (int nib = 0; nib < 8; ++nib) {
-        int off;
-        if (PACK == QK_PACK_U32X8)
-          off = 8 * i + nib;
-        else
-          off = ((nib & 1) ? hg : 0) + 4 * i + (nib >> 1);
+        const int off = PACK == QK_PACK_U32X8
+                            ? 8 * i + nib
+                            : ((nib & 1) ? 16 : 0) + 4 * i + (nib >> 1);
         const float q = static_cast<float>((word >> (4 * nib)) & 15u);
-        out[off] = from_f32<OT>(__fadd_rn(__fmul_rn(q, s), b));
+        v[off] = __fadd_rn(__fmul_rn(q, s), b);
       }
     } else {
 #pragma unroll
@@ -394,9 +416,32 @@ __global__ void dequant_kernel(QmvArgs a, long long total_chunks) {
           q = static_cast<float>(static_cast<int8_t>(word >> (8 * bt)));
         else
           q = static_cast<float>((word >> (8 * bt)) & 255u);
-        out[4 * i + bt] = from_f32<OT>(__fadd_rn(__fmul_rn(q, s), b));
+        v[4 * i + bt] = __fadd_rn(__fmul_rn(q, s), b);
       }
     }
+  }
+  // Runs of 16 values: whole 16-byte stores when the output allows them
+  // (a.out_vec), else element by element.
+#pragma unroll
+  for (int r = 0; r < kCodes / 16; ++r) {
+    OT* dst = out + (PACK == QK_PACK_BYTE_HALFSPLIT ? r * hg : r * 16);
+    if (a.out_vec) {
+      constexpr int kPer = 16 / sizeof(OT);
+#pragma unroll
+      for (int q = 0; q < 16 / kPer; ++q) {
+        union {
+          u32x4 u;
+          OT e[kPer];
+        } o;
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) o.e[e] = from_f32<OT>(v[16 * r + kPer * q + e]);
+        *reinterpret_cast<u32x4*>(dst + kPer * q) = o.u;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) dst[e] = from_f32<OT>(v[16 * r + e]);
+    }
+  }
   }
 }
 
@@ -1354,6 +1399,8 @@ QmvArgs MakeArgs(const QuantProblem& p) {
   a.bdt = p.bias_dtype;
   a.has_bias = p.has_bias;
   a.row_bytes = RowBytes(p);
+  a.gather = static_cast<const int*>(p.rows);
+  a.out_vec = 0;
   return a;
 }
 
@@ -1437,22 +1484,26 @@ qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream) {
 qk_status LaunchDequantize(const QuantProblem& p, hipStream_t stream) {
   if (qk_status s = CheckLimits(p); s != QK_OK) return s;
   QmvArgs a = MakeArgs(p);
-  const long long chunks = p.n * (a.row_bytes / 16);
+  // Every 16-value run starts at a multiple of 8 elements of its row.
+  a.out_vec = reinterpret_cast<uintptr_t>(p.y) % 16 == 0 &&
+              (p.k * DTypeSize(p.y_dtype)) % 16 == 0 && p.group % 16 == 0;
+  const long long chunks =
+      (p.rows != nullptr ? p.rows_n : p.n) * (a.row_bytes / 16);
   dim3 block(256), grid(static_cast<unsigned>((chunks + 255) / 256));
 #define QK_DQ(OT)                                                              \
   switch (p.packing) {                                                         \
     case QK_PACK_U32X8:                                                        \
-      dequant_kernel<QK_PACK_U32X8, OT><<<grid, block, 0, stream>>>(a, chunks); \
+      dequant_kernel<QK_PACK_U32X8, OT, 1><<<grid, block, 0, stream>>>(a, chunks); \
       break;                                                                   \
     case QK_PACK_BYTE_HALFSPLIT:                                               \
-      dequant_kernel<QK_PACK_BYTE_HALFSPLIT, OT>                               \
+      dequant_kernel<QK_PACK_BYTE_HALFSPLIT, OT, 1>                            \
           <<<grid, block, 0, stream>>>(a, chunks);                             \
       break;                                                                   \
     case QK_PACK_U8:                                                           \
-      dequant_kernel<QK_PACK_U8, OT><<<grid, block, 0, stream>>>(a, chunks);    \
+      dequant_kernel<QK_PACK_U8, OT, 1><<<grid, block, 0, stream>>>(a, chunks);    \
       break;                                                                   \
     default:                                                                   \
-      dequant_kernel<QK_PACK_S8_SYM, OT><<<grid, block, 0, stream>>>(a, chunks); \
+      dequant_kernel<QK_PACK_S8_SYM, OT, 1><<<grid, block, 0, stream>>>(a, chunks); \
   }
   if (p.y_dtype == QK_BF16) {
     QK_DQ(bf16)
@@ -1462,7 +1513,47 @@ qk_status LaunchDequantize(const QuantProblem& p, hipStream_t stream) {
     QK_DQ(float)
   }
 #undef QK_DQ
-  return PostLaunch("dequantize");
+  return PostLaunch(p.rows != nullptr ? "embed_dequantize" : "dequantize");
+}
+
+namespace {
+// One thread per 16-byte chunk of an output row: out[t] = table[rows[t]].
+__global__ void row_gather_kernel(const uint8_t* table, long long ld_bytes,
+                                  int n, int row_chunks, const int* rows,
+                                  long long total, uint8_t* out) {
+  const long long t = static_cast<long long>(blockIdx.x) * blockDim.x +
+                      threadIdx.x;
+  if (t >= total) return;
+  const long long orow = t / row_chunks;
+  const int c = static_cast<int>(t % row_chunks);
+  const int r = min(max(rows[orow], 0), n - 1);
+  *reinterpret_cast<u32x4*>(out + (orow * row_chunks + c) * 16) =
+      *reinterpret_cast<const u32x4*>(table + r * ld_bytes + c * 16);
+}
+}  // namespace
+
+qk_status LaunchRowGather(const void* table, int64_t n, int64_t k, int64_t ld,
+                          int esz, const void* rows, int64_t rows_n, void* out,
+                          hipStream_t stream) {
+  const int64_t row_bytes = k * esz;
+  if (row_bytes % 16 != 0 || (ld * esz) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(table) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(out) % 16 != 0) {
+    return Fail(QK_UNIMPLEMENTED,
+                "qkern: embedding gather needs 16-byte aligned tables, "
+                "outputs and rows");
+  }
+  if (n > 0x7fffffff || row_bytes / 16 > 0x7fffffff) {
+    return Fail(QK_UNIMPLEMENTED, "qkern: embedding table too large");
+  }
+  const long long total = rows_n * (row_bytes / 16);
+  if (total == 0) return QK_OK;
+  row_gather_kernel<<<static_cast<unsigned>((total + 255) / 256), 256, 0,
+                      stream>>>(
+      static_cast<const uint8_t*>(table), ld * esz, static_cast<int>(n),
+      static_cast<int>(row_bytes / 16), static_cast<const int*>(rows), total,
+      static_cast<uint8_t*>(out));
+  return PostLaunch("embed_gather");
 }
 
 }  // namespace qk

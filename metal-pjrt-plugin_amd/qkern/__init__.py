@@ -14,7 +14,8 @@ from .blas import (BlasLt, Epilogue, GemmConfig, MatmulPlan,  # noqa: F401
                    MatrixLayout, MemoryArgs, Order, matmul)
 from .ffi import (Packing, RownormKind, decode_attention,  # noqa: F401
                   decode_attention_noalloc,
-                  decode_attention_workspace_size, dequantize, layer_norm,
+                  decode_attention_workspace_size, dequantize, embed,
+                  layer_norm,
                   qmatvec, rms_norm, rownorm, softmax)
 
 

@@ -77,6 +77,9 @@ SIGNATURES = {
     "qk_qmatvec": (ctypes.c_int, [ctypes.c_void_p, _P(BufferC), _P(BufferC),
                                   _P(BufferC), _P(BufferC), _P(BufferC),
                                   _P(QuantAttrsC)]),
+    "qk_embed": (ctypes.c_int, [ctypes.c_void_p, _P(BufferC), _P(BufferC),
+                                _P(BufferC), _P(BufferC), _P(BufferC),
+                                _P(QuantAttrsC)]),
     "qk_dequantize": (ctypes.c_int, [ctypes.c_void_p, _P(BufferC), _P(BufferC),
                                      _P(BufferC), _P(BufferC),
                                      _P(QuantAttrsC)]),

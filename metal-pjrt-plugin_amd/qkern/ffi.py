@@ -99,6 +99,30 @@ def dequantize(codes, scales, biases=None, *, k, packing=Packing.U32X8,
     return out
 
 
+def embed(table, tokens, scales=None, biases=None, *, k=None,
+          packing=Packing.U32X8, group_size=64, dtype=None, out=None,
+          stream=None):
+    """qk$embed: qwen3.embed (examples/llm/qwen3.py:270-274), the rows of
+    `table` picked by int32 `tokens`, [*tokens.shape, K]. With scales the
+    table holds codes (k: the row length, required) and each row is
+    dequantized to `dtype` (default: the scales' type, as the reference
+    does); without, it is a dense [V, K] table copied in its own type.
+    Tokens outside the table are clamped."""
+    if scales is None:
+        k = table.shape[1]
+        dtype = table.dtype
+    elif dtype is None:
+        dtype = scales.dtype
+    if out is None:
+        out = torch.empty(*tokens.shape, k, dtype=dtype, device=table.device)
+    bt, bw, bs, bb, bo = (any_buffer(t) for t in (tokens, table, scales,
+                                                   biases, out))
+    attrs = _attrs(packing, group_size, biases is not None)
+    check(lib().qk_embed(stream_handle(stream), _ref(bt), _ref(bw), _ref(bs),
+                         _ref(bb), _ref(bo), ctypes.byref(attrs)))
+    return out
+
+
 def rownorm(x, kind, *, eps=1e-6, gain=None, beta=None, out=None,
             stream=None):
     """qk$rownorm over the last dimension of x (RMS, LAYER or SOFTMAX)."""

@@ -277,6 +277,18 @@ def matvec_int8_reference_form(x, q, s):
 # (qwen3.py:325,330), bench/jax_bench.py:44-46 (layernorm: biased variance).
 
 
+def embed(table, tokens):
+    """qwen3.embed (examples/llm/qwen3.py:270-274): the rows of `table`
+    picked by `tokens`, shaped [*tokens.shape, K]. For a quantized table the
+    reference gathers the q4/q, s and b rows and dequantizes them
+    (qwen3.py:271); dequantization is per row, so that equals the rows of
+    the dequantized table, which is what `table` is here. Indices outside
+    [0, V) are clamped, as a JAX gather clamps them."""
+    table = np.asarray(table)
+    idx = np.clip(np.asarray(tokens, np.int64), 0, table.shape[0] - 1)
+    return table[idx.reshape(-1)].reshape(*np.shape(tokens), table.shape[1])
+
+
 def rms_norm(x, w=None, eps=1e-6):
     x = np.asarray(x, dtype=np.float64)
     y = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)

@@ -371,3 +371,31 @@ def test_decode_attention_argument_checks():
     # an empty batch launches nothing
     qkern.decode_attention(q[:0], k[:0], v[:0], pos,
                            workspace=torch.zeros(16, dtype=torch.uint8))
+
+
+def test_embed_argument_checks():
+    # shapes and types are checked before any launch (host tensors stand in
+    # for device buffers)
+    def status(fn):
+        try:
+            fn()
+            return _lib.OK, ""
+        except qkern.QkError as e:
+            return e.status, e.message
+
+    codes = torch.zeros(10, 64, dtype=torch.int32)  # [V, K/8], K = 512
+    s = torch.zeros(10, 8, dtype=torch.bfloat16)
+    tok = torch.zeros(3, dtype=torch.int32)
+    st, msg = status(lambda: qkern.embed(codes, tok.float(), s, k=512))
+    assert st == _lib.INVALID_ARGUMENT and "int32" in msg
+    st, msg = status(lambda: qkern.embed(
+        codes, tok, s, k=512, out=torch.zeros(4, 512, dtype=torch.bfloat16)))
+    assert st == _lib.INVALID_ARGUMENT and "tokens" in msg
+    st, msg = status(lambda: qkern.embed(codes, tok, s, k=256))
+    assert st == _lib.INVALID_ARGUMENT
+    table = torch.zeros(10, 64, dtype=torch.bfloat16)
+    st, msg = status(lambda: qkern.embed(
+        table, tok, out=torch.zeros(3, 64, dtype=torch.float32)))
+    assert st == _lib.INVALID_ARGUMENT and "dense embedding table" in msg
+    # empty token arrays launch nothing
+    qkern.embed(table, tok[:0])

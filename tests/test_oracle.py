@@ -409,3 +409,26 @@ def test_decode_attention_oracle():
     # dropped scale would be caught
     assert not np.allclose(O.decode_attention(q, k, v, 7, 0.7),
                            O.decode_attention(q, k, v, 7, 1.0))
+
+
+def test_embed_gathers_dequantized_rows_and_clamps():
+    # qwen3.embed gathers the q4, s and b rows, then dequantizes
+    # (qwen3.py:270-274): the same as picking rows of the dequantized table
+    rng = np.random.default_rng(3)
+    v, k = 9, 128
+    codes = rng.integers(0, 16, size=(v, k)).astype(np.float32)
+    s = O.bf16_round(rng.uniform(0.001, 0.02, (v, k // 64)).astype(np.float32))
+    b = O.bf16_round(0.05 * rng.standard_normal((v, k // 64)).astype(np.float32))
+    tokens = np.array([[3, 0, 8], [8, 8, 1]])
+    gathered = O.dequantize_f32(codes[tokens.reshape(-1)].reshape(-1, 2, 64),
+                                s[tokens.reshape(-1)][..., None],
+                                b[tokens.reshape(-1)][..., None])
+    table = O.dequantize_f32(codes.reshape(v, 2, 64), s[..., None],
+                             b[..., None])
+    got = O.embed(table, tokens)
+    assert got.shape == (2, 3, k)
+    assert np.array_equal(got.reshape(-1, k), gathered)
+    # identity gather, and clamping of indices outside [0, V)
+    assert np.array_equal(O.embed(table, np.arange(v)), table)
+    assert np.array_equal(O.embed(table, [-5, v, 10 ** 6]),
+                          table[[0, v - 1, v - 1]])
