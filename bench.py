@@ -146,123 +146,136 @@ def gemm_vs_library(torch, ours, library, iters=20, reps=4, warm_s=0.25):
     return sorted(mine)[reps // 2], sorted(lib)[reps // 2]
 
 
+# Secondary parts to run (bench.py --only PART[,PART]); all by default.
+ONLY = None
+
+
+def want(part):
+    return ONLY is None or part in ONLY
+
+
 def secondary(torch, qkern, dev, gen):
     out = []
-    # bf16 GEMM + bias + SiLU (C3), NN row-major: D = silu(A @ B + bias)
-    for (m, n, k) in [(4096, 4096, 4096), (2048, 12288, 4096),
-                      (2048, 4096, 12288)]:
-        a = (torch.randn(m, k, device=dev, generator=gen) / k ** 0.5).to(
-            torch.bfloat16)
-        b = (torch.randn(k, n, device=dev, generator=gen) / k ** 0.5).to(
-            torch.bfloat16)
-        bias = (0.02 * torch.randn(n, device=dev, generator=gen)).to(
-            torch.bfloat16)
-        d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    if want("gemm"):
+        # bf16 GEMM + bias + SiLU (C3), NN row-major: D = silu(A @ B + bias)
+        for (m, n, k) in [(4096, 4096, 4096), (2048, 12288, 4096),
+                          (2048, 4096, 12288)]:
+            a = (torch.randn(m, k, device=dev, generator=gen) / k ** 0.5).to(
+                torch.bfloat16)
+            b = (torch.randn(k, n, device=dev, generator=gen) / k ** 0.5).to(
+                torch.bfloat16)
+            bias = (0.02 * torch.randn(n, device=dev, generator=gen)).to(
+                torch.bfloat16)
+            d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            L = qkern.blas
+            lay = lambda r, c: L.MatrixLayout("bfloat16", r, c)
+            plan = L.BlasLt.get_matmul_plan(
+                L.GemmConfig(lay(m, k), lay(k, n), lay(m, n), lay(m, n)),
+                L.Epilogue.kBiasThenSILU)
+            args = L.MemoryArgs(a, b, None, d, bias)
+            for _ in range(3):
+                plan.execute_on_stream(None, args)
+            # hipBLASLt (torch.matmul, no epilogue) on the same operands, timed
+            # alternately with it
+            ms, ms_lt = gemm_vs_library(
+                torch, lambda i: plan.execute_on_stream(None, args),
+                lambda: torch.matmul(a, b, out=d))
+            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            out.append({"name": f"bf16 gemm+bias+silu {m}x{n}x{k}",
+                        "value": round(tf, 1), "unit": "TFLOP/s",
+                        "ms": round(ms, 4), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                        "kernel": plan.describe().split("kernel=")[-1],
+                        "hipblaslt_matmul_tflops": round(
+                            2.0 * m * n * k / (ms_lt * 1e-3) / 1e12, 1)})
+            del a, b, d
+    if want("f32"):
+        # f32 GEMM C = A @ B at 1024^3 (C1), MFMA f32 peak
+        n = 1024
+        a = torch.randn(n, n, device=dev, generator=gen)
+        b = torch.randn(n, n, device=dev, generator=gen)
+        d = torch.empty(n, n, device=dev)
         L = qkern.blas
-        lay = lambda r, c: L.MatrixLayout("bfloat16", r, c)
+        lay = lambda r, c: L.MatrixLayout("float32", r, c)
         plan = L.BlasLt.get_matmul_plan(
-            L.GemmConfig(lay(m, k), lay(k, n), lay(m, n), lay(m, n)),
-            L.Epilogue.kBiasThenSILU)
-        args = L.MemoryArgs(a, b, None, d, bias)
-        for _ in range(3):
-            plan.execute_on_stream(None, args)
-        # hipBLASLt (torch.matmul, no epilogue) on the same operands, timed
-        # alternately with it
-        ms, ms_lt = gemm_vs_library(
-            torch, lambda i: plan.execute_on_stream(None, args),
-            lambda: torch.matmul(a, b, out=d))
-        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        out.append({"name": f"bf16 gemm+bias+silu {m}x{n}x{k}",
-                    "value": round(tf, 1), "unit": "TFLOP/s",
-                    "ms": round(ms, 4), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
-                    "kernel": plan.describe().split("kernel=")[-1],
-                    "hipblaslt_matmul_tflops": round(
-                        2.0 * m * n * k / (ms_lt * 1e-3) / 1e12, 1)})
+            L.GemmConfig(lay(n, n), lay(n, n), lay(n, n), lay(n, n)),
+            L.Epilogue.kDefault)
+        args = L.MemoryArgs(a, b, None, d)
+        plan.execute_on_stream(None, args)
+        ms = timed_launches(torch, lambda i: plan.execute_on_stream(None, args), 20)
+        tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+        out.append({"name": "f32 gemm 1024x1024x1024", "value": round(tf, 1),
+                    "unit": "TFLOP/s", "ms": round(ms, 4),
+                    "frac": round(tf / F32_PEAK_TFLOPS, 4),
+                    "kernel": plan.describe().split("kernel=")[-1]})
         del a, b, d
-    # f32 GEMM C = A @ B at 1024^3 (C1), MFMA f32 peak
-    n = 1024
-    a = torch.randn(n, n, device=dev, generator=gen)
-    b = torch.randn(n, n, device=dev, generator=gen)
-    d = torch.empty(n, n, device=dev)
-    L = qkern.blas
-    lay = lambda r, c: L.MatrixLayout("float32", r, c)
-    plan = L.BlasLt.get_matmul_plan(
-        L.GemmConfig(lay(n, n), lay(n, n), lay(n, n), lay(n, n)),
-        L.Epilogue.kDefault)
-    args = L.MemoryArgs(a, b, None, d)
-    plan.execute_on_stream(None, args)
-    ms = timed_launches(torch, lambda i: plan.execute_on_stream(None, args), 20)
-    tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
-    out.append({"name": "f32 gemm 1024x1024x1024", "value": round(tf, 1),
-                "unit": "TFLOP/s", "ms": round(ms, 4),
-                "frac": round(tf / F32_PEAK_TFLOPS, 4),
-                "kernel": plan.describe().split("kernel=")[-1]})
-    del a, b, d
-    # int4 batched rows (decode batch / prefill) at 12288 x 4096
-    n, k = 12288, 4096
-    sets = [make_int4(torch, dev, n, k, gen) for _ in range(8)]
-    for m in (16, 512):
-        x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
-        y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-        fn = lambda i: qkern.qmatvec(x, *sets[i % 8], out=y)
-        fn(0)
-        ms = timed_launches(torch, fn, 16)
-        gbs = int4_bytes(m, n, k) / (ms * 1e-3) / 1e9
-        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        out.append({"name": f"int4 g64 qmatvec M={m} {n}x{k}",
-                    "value": round(gbs, 1), "unit": "GB/s",
-                    "tflops": round(tf, 2), "ms": round(ms, 4),
-                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
-    del sets
-    # int8 affine GEMV (C4)
-    n, k = 12288, 4096
-    sets8 = []
-    for _ in range(12):
-        codes = torch.randint(0, 256, (n, k), dtype=torch.uint8, device=dev,
-                              generator=gen)
-        s = (torch.rand(n, k // GROUP, device=dev, generator=gen) * 0.019 +
-             0.001).to(torch.bfloat16)
-        b = (0.05 * torch.randn(n, k // GROUP, device=dev, generator=gen)).to(
-            torch.bfloat16)
-        sets8.append((codes, s, b))
-    for m in (1, 8, 128):
-        x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
-        y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-        fn = lambda i: qkern.qmatvec(x, *sets8[i % 12], out=y,
-                                     packing=qkern.Packing.U8)
-        fn(0)
-        ms = timed_launches(torch, fn, 24)
-        gbs = int8_bytes(m, n, k) / (ms * 1e-3) / 1e9
-        out.append({"name": f"int8 affine g64 qmatvec M={m} {n}x{k}",
-                    "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
-                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
-    del sets8
-    # rownorm [4096, 4096]
-    # (LayerNorm with gain and offset, eps 1e-5, beside the configured
-    # RMSNorm and softmax)
-    for name, kind, dt, esz in [("rmsnorm bf16", 0, torch.bfloat16, 2),
-                                ("rmsnorm f32", 0, torch.float32, 4),
-                                ("softmax f32", 2, torch.float32, 4),
-                                ("layernorm bf16", 1, torch.bfloat16, 2)]:
-        xs = [torch.randn(4096, 4096, device=dev, generator=gen).to(dt)
-              for _ in range(8)]
-        ys = [torch.empty_like(xs[0]) for _ in range(2)]
-        g = (1 + 0.1 * torch.randn(4096, device=dev, generator=gen))
-        bt = 0.1 * torch.randn(4096, device=dev, generator=gen)
-        gain = g if kind != 2 else None
-        beta = bt if kind == 1 else None
-        eps = 1e-5 if kind == 1 else 1e-6
-        fn = lambda i: qkern.rownorm(xs[i % 8], kind, eps=eps, gain=gain,
-                                     beta=beta, out=ys[i % 2])
-        fn(0)
-        ms = timed_launches(torch, fn, 32)
-        nbytes = (2 * 4096 * 4096 * esz + (4096 * 4 if kind != 2 else 0) +
-                  (4096 * 4 if kind == 1 else 0))
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        out.append({"name": f"{name} 4096x4096", "value": round(gbs, 1),
-                    "unit": "GB/s", "ms": round(ms, 4),
-                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
-        del xs, ys
+    if want("int4"):
+        # int4 batched rows (decode batch / prefill) at 12288 x 4096
+        n, k = 12288, 4096
+        sets = [make_int4(torch, dev, n, k, gen) for _ in range(8)]
+        for m in (16, 512):
+            x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            fn = lambda i: qkern.qmatvec(x, *sets[i % 8], out=y)
+            fn(0)
+            ms = timed_launches(torch, fn, 16)
+            gbs = int4_bytes(m, n, k) / (ms * 1e-3) / 1e9
+            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            out.append({"name": f"int4 g64 qmatvec M={m} {n}x{k}",
+                        "value": round(gbs, 1), "unit": "GB/s",
+                        "tflops": round(tf, 2), "ms": round(ms, 4),
+                        "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del sets
+    if want("int8"):
+        # int8 affine GEMV (C4)
+        n, k = 12288, 4096
+        sets8 = []
+        for _ in range(12):
+            codes = torch.randint(0, 256, (n, k), dtype=torch.uint8, device=dev,
+                                  generator=gen)
+            s = (torch.rand(n, k // GROUP, device=dev, generator=gen) * 0.019 +
+                 0.001).to(torch.bfloat16)
+            b = (0.05 * torch.randn(n, k // GROUP, device=dev, generator=gen)).to(
+                torch.bfloat16)
+            sets8.append((codes, s, b))
+        for m in (1, 8, 128):
+            x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            fn = lambda i: qkern.qmatvec(x, *sets8[i % 12], out=y,
+                                         packing=qkern.Packing.U8)
+            fn(0)
+            ms = timed_launches(torch, fn, 24)
+            gbs = int8_bytes(m, n, k) / (ms * 1e-3) / 1e9
+            out.append({"name": f"int8 affine g64 qmatvec M={m} {n}x{k}",
+                        "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
+                        "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del sets8
+    if want("rownorm"):
+        # rownorm [4096, 4096]
+        # (LayerNorm with gain and offset, eps 1e-5, beside the configured
+        # RMSNorm and softmax)
+        for name, kind, dt, esz in [("rmsnorm bf16", 0, torch.bfloat16, 2),
+                                    ("rmsnorm f32", 0, torch.float32, 4),
+                                    ("softmax f32", 2, torch.float32, 4),
+                                    ("layernorm bf16", 1, torch.bfloat16, 2)]:
+            xs = [torch.randn(4096, 4096, device=dev, generator=gen).to(dt)
+                  for _ in range(8)]
+            ys = [torch.empty_like(xs[0]) for _ in range(2)]
+            g = (1 + 0.1 * torch.randn(4096, device=dev, generator=gen))
+            bt = 0.1 * torch.randn(4096, device=dev, generator=gen)
+            gain = g if kind != 2 else None
+            beta = bt if kind == 1 else None
+            eps = 1e-5 if kind == 1 else 1e-6
+            fn = lambda i: qkern.rownorm(xs[i % 8], kind, eps=eps, gain=gain,
+                                         beta=beta, out=ys[i % 2])
+            fn(0)
+            ms = timed_launches(torch, fn, 32)
+            nbytes = (2 * 4096 * 4096 * esz + (4096 * 4 if kind != 2 else 0) +
+                      (4096 * 4 if kind == 1 else 0))
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            out.append({"name": f"{name} 4096x4096", "value": round(gbs, 1),
+                        "unit": "GB/s", "ms": round(ms, 4),
+                        "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            del xs, ys
     return out
 
 
@@ -270,96 +283,100 @@ def secondary_more(torch, qkern, dev, gen):
     """Few-row dense GEMMs, decode attention and the device copy ceiling."""
     out = []
     L = qkern.blas
-    # The reference's few-row list (docs/performance.md:223-242,
-    # examples/llm/skinny_jax.py): 28 GEMMs x[M, 1024] @ W.T, bf16
-    # W [6144, 1024] (28 distinct weights, 352 MB), one call = all 28.
-    nl, kk, nn = 28, 1024, 6144
-    ws = [(0.02 * torch.randn(nn, kk, device=dev, generator=gen)).to(
-        torch.bfloat16) for _ in range(nl)]
-    for m in (1, 2, 4, 8, 16, 32, 64):
-        x = (0.01 * torch.ones(m, kk, device=dev)).to(torch.bfloat16)
-        ys = [torch.empty(m, nn, dtype=torch.bfloat16, device=dev)
-              for _ in range(nl)]
-        plan = L.BlasLt.get_matmul_plan(
-            L.GemmConfig(L.MatrixLayout("bfloat16", m, kk),
-                         L.MatrixLayout("bfloat16", kk, nn,
-                                        L.Order.kColumnMajor, 1, kk, 0),
-                         L.MatrixLayout("bfloat16", m, nn),
-                         L.MatrixLayout("bfloat16", m, nn)),
-            L.Epilogue.kDefault)
+    if want("fewrow"):
+        # The reference's few-row list (docs/performance.md:223-242,
+        # examples/llm/skinny_jax.py): 28 GEMMs x[M, 1024] @ W.T, bf16
+        # W [6144, 1024] (28 distinct weights, 352 MB), one call = all 28.
+        nl, kk, nn = 28, 1024, 6144
+        ws = [(0.02 * torch.randn(nn, kk, device=dev, generator=gen)).to(
+            torch.bfloat16) for _ in range(nl)]
+        for m in (1, 2, 4, 8, 16, 32, 64):
+            x = (0.01 * torch.ones(m, kk, device=dev)).to(torch.bfloat16)
+            ys = [torch.empty(m, nn, dtype=torch.bfloat16, device=dev)
+                  for _ in range(nl)]
+            plan = L.BlasLt.get_matmul_plan(
+                L.GemmConfig(L.MatrixLayout("bfloat16", m, kk),
+                             L.MatrixLayout("bfloat16", kk, nn,
+                                            L.Order.kColumnMajor, 1, kk, 0),
+                             L.MatrixLayout("bfloat16", m, nn),
+                             L.MatrixLayout("bfloat16", m, nn)),
+                L.Epilogue.kDefault)
 
-        def call(i, x=x, ys=ys, plan=plan):
-            for j in range(nl):
-                plan.execute_on_stream(None, L.MemoryArgs(x, ws[j], None,
-                                                          ys[j]))
-        ms = timed_launches(torch, call, 4)
-        nbytes = nl * (nn * kk * 2 + m * kk * 2 + m * nn * 2)
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        out.append({"name": f"bf16 few-row gemm list 28x[{m},1024]x"
-                            f"[1024,6144]^T", "value": round(gbs, 1),
-                    "unit": "GB/s", "ms": round(ms, 4),
-                    "frac": round(gbs / HBM_PEAK_GBS, 4),
-                    "kernel": plan.describe().split("kernel=")[-1]})
-    del ws
-    # Decode attention at Qwen3-8B's shape (32 query heads over 8 KV heads
-    # of dim 128), one sequence, the whole cache attended: K + V read once
-    for smax in (4096, 32768):
-        b, kv, g, d = 1, 8, 4, 128
-        nset = max(2, -(-(512 << 20) // (2 * b * kv * smax * d * 2)))
-        caches = [(torch.randn(b, kv, smax, d, device=dev, generator=gen).to(
-            torch.bfloat16), torch.randn(b, kv, d, smax, device=dev,
-                                         generator=gen).to(torch.bfloat16))
-            for _ in range(nset)]
-        q = torch.randn(b, kv, g, d, device=dev, generator=gen).to(
-            torch.bfloat16)
-        pos = torch.tensor([smax - 1], dtype=torch.int32, device=dev)
-        o = torch.empty_like(q)
-        wsp = torch.empty(qkern.decode_attention_workspace_size(
-            q, caches[0][0]), dtype=torch.uint8, device=dev)
-        fn = lambda i: qkern.decode_attention(q, *caches[i % nset], pos,
-                                              workspace=wsp, out=o)
+            def call(i, x=x, ys=ys, plan=plan):
+                for j in range(nl):
+                    plan.execute_on_stream(None, L.MemoryArgs(x, ws[j], None,
+                                                              ys[j]))
+            ms = timed_launches(torch, call, 4)
+            nbytes = nl * (nn * kk * 2 + m * kk * 2 + m * nn * 2)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            out.append({"name": f"bf16 few-row gemm list 28x[{m},1024]x"
+                                f"[1024,6144]^T", "value": round(gbs, 1),
+                        "unit": "GB/s", "ms": round(ms, 4),
+                        "frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "kernel": plan.describe().split("kernel=")[-1]})
+        del ws
+    if want("attention"):
+        # Decode attention at Qwen3-8B's shape (32 query heads over 8 KV heads
+        # of dim 128), one sequence, the whole cache attended: K + V read once
+        for smax in (4096, 32768):
+            b, kv, g, d = 1, 8, 4, 128
+            nset = max(2, -(-(512 << 20) // (2 * b * kv * smax * d * 2)))
+            caches = [(torch.randn(b, kv, smax, d, device=dev, generator=gen).to(
+                torch.bfloat16), torch.randn(b, kv, d, smax, device=dev,
+                                             generator=gen).to(torch.bfloat16))
+                for _ in range(nset)]
+            q = torch.randn(b, kv, g, d, device=dev, generator=gen).to(
+                torch.bfloat16)
+            pos = torch.tensor([smax - 1], dtype=torch.int32, device=dev)
+            o = torch.empty_like(q)
+            wsp = torch.empty(qkern.decode_attention_workspace_size(
+                q, caches[0][0]), dtype=torch.uint8, device=dev)
+            fn = lambda i: qkern.decode_attention(q, *caches[i % nset], pos,
+                                                  workspace=wsp, out=o)
+            fn(0)
+            ms = timed_launches(torch, fn, 32)
+            nbytes = 2 * b * kv * smax * d * 2 + 2 * q.numel() * 2
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            out.append({"name": f"decode attention bf16 B=1 KV=8 G=4 D=128 "
+                                f"S={smax}", "value": round(gbs, 1),
+                        "unit": "GB/s", "ms": round(ms, 4),
+                        "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            del caches
+    if want("embed"):
+        # Quantized token embedding (qwen3.embed) of Qwen3-8B's int4 table
+        # (151936 x 4096, group 64): 2048 prefill tokens; bytes = the rows'
+        # codes, scales and offsets read and the bf16 rows written
+        n, k = 151936, 4096
+        words, s, b = make_int4(torch, dev, n, k, gen)
+        tok = torch.randint(0, n, (2048,), dtype=torch.int32, device=dev,
+                            generator=gen)
+        rows = torch.empty(2048, k, dtype=torch.bfloat16, device=dev)
+        fn = lambda i: qkern.embed(words, tok, s, b, k=k, out=rows)
         fn(0)
         ms = timed_launches(torch, fn, 32)
-        nbytes = 2 * b * kv * smax * d * 2 + 2 * q.numel() * 2
+        nbytes = 2048 * (k // 2 + (k // GROUP) * 4 + k * 2) + 2048 * 4
         gbs = nbytes / (ms * 1e-3) / 1e9
-        out.append({"name": f"decode attention bf16 B=1 KV=8 G=4 D=128 "
-                            f"S={smax}", "value": round(gbs, 1),
-                    "unit": "GB/s", "ms": round(ms, 4),
+        out.append({"name": "int4 embed gather 2048 tokens of 151936x4096",
+                    "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
                     "frac": round(gbs / HBM_PEAK_GBS, 4)})
-        del caches
-    # Quantized token embedding (qwen3.embed) of Qwen3-8B's int4 table
-    # (151936 x 4096, group 64): 2048 prefill tokens; bytes = the rows'
-    # codes, scales and offsets read and the bf16 rows written
-    n, k = 151936, 4096
-    words, s, b = make_int4(torch, dev, n, k, gen)
-    tok = torch.randint(0, n, (2048,), dtype=torch.int32, device=dev,
-                        generator=gen)
-    rows = torch.empty(2048, k, dtype=torch.bfloat16, device=dev)
-    fn = lambda i: qkern.embed(words, tok, s, b, k=k, out=rows)
-    fn(0)
-    ms = timed_launches(torch, fn, 32)
-    nbytes = 2048 * (k // 2 + (k // GROUP) * 4 + k * 2) + 2048 * 4
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    out.append({"name": "int4 embed gather 2048 tokens of 151936x4096",
-                "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
-                "frac": round(gbs / HBM_PEAK_GBS, 4)})
-    del words, s, b, rows
-    # The practical read+write ceiling: a plain device copy of the rownorm
-    # sizes (rotating over 8 sources, 537 MB or more)
-    for mb, dt in ((67, torch.bfloat16), (134, torch.float32)):
-        srcs = [torch.empty(4096, 4096, dtype=dt, device=dev).normal_(
-            generator=gen) for _ in range(8)]
-        dst = torch.empty_like(srcs[0])
-        fn = lambda i: dst.copy_(srcs[i % 8])
-        fn(0)
-        ms = timed_launches(torch, fn, 32)
-        nbytes = 2 * srcs[0].numel() * srcs[0].element_size()
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        out.append({"name": f"device copy 4096x4096 {str(dt)[6:]} "
-                            f"(read+write {2 * mb} MB)", "value": round(gbs, 1),
-                    "unit": "GB/s", "ms": round(ms, 4),
-                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
-        del srcs
+        del words, s, b, rows
+    if want("copy"):
+        # The practical read+write ceiling: a plain device copy of the rownorm
+        # sizes (rotating over 8 sources, 537 MB or more)
+        for mb, dt in ((67, torch.bfloat16), (134, torch.float32)):
+            srcs = [torch.empty(4096, 4096, dtype=dt, device=dev).normal_(
+                generator=gen) for _ in range(8)]
+            dst = torch.empty_like(srcs[0])
+            fn = lambda i: dst.copy_(srcs[i % 8])
+            fn(0)
+            ms = timed_launches(torch, fn, 32)
+            nbytes = 2 * srcs[0].numel() * srcs[0].element_size()
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            out.append({"name": f"device copy 4096x4096 {str(dt)[6:]} "
+                                f"(read+write {2 * mb} MB)", "value": round(gbs, 1),
+                        "unit": "GB/s", "ms": round(ms, 4),
+                        "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            del srcs
     return out
 
 
@@ -454,6 +471,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default=None,
+                    help="run only these secondary parts (comma list of "
+                         "gemm, f32, int4, int8, rownorm, fewrow, attention, "
+                         "embed, copy) and print them, without the headline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 plain device copies of 512 MiB (the "
                          "reference kernel for FETCH_SIZE/WRITE_SIZE scaling)")
@@ -479,6 +500,13 @@ def main():
                           "copy_bytes_written": dst.numel() * 4}))
         return
     gen = torch.Generator(device=dev).manual_seed(0)
+    if args.only:
+        global ONLY
+        ONLY = set(args.only.split(","))
+        for r in (secondary(torch, qkern, dev, gen) +
+                  secondary_more(torch, qkern, dev, gen)):
+            print(json.dumps(r), flush=True)
+        return
     rot = 3
     sets = [[make_int4(torch, dev, n, k, gen) for (n, k) in QWEN3_8B]
             for _ in range(rot)]
