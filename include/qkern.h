@@ -202,7 +202,13 @@ typedef struct {
  * type into y [..., N]. scales/biases [N, K/g] (trailing 1 allowed) in f32,
  * f16 or bf16. Replaces the reduction fusions XLA emits for _matvec_int8 /
  * _matvec_int4 (examples/llm/qwen3.py:233-267) and, for rows beyond the
- * matvec range, linear()'s dequantize-then-einsum (qwen3.py:218-230). */
+ * matvec range, linear()'s dequantize-then-einsum (qwen3.py:218-230).
+ * For many rows (65 and up) on few weight rows the library may split K
+ * over workgroups; the partial sums then go through a workspace it owns,
+ * one per (device, stream), allocated on the first such call on a stream
+ * and grown (never freed) when a larger one is needed. Such a call on a
+ * stream that is being captured and has no large enough workspace yet
+ * takes the unsplit kernel instead. Results do not depend on the split. */
 qk_status qk_qmatvec(void* stream, const qk_buffer* x, const qk_buffer* codes,
                      const qk_buffer* scales, const qk_buffer* biases,
                      qk_buffer* y, const qk_quant_attrs* attrs);

@@ -42,6 +42,11 @@ struct GemmArgs {
   const void* qscale;
   const void* qbias;
   int qsdt, qbdt, qhas_bias, qgroup, qrow_bytes;
+  // Split K (qgemm_dma.h): K ranges per tile (1: none), the f32 partial
+  // tiles and the per-tile arrival counters (zero between launches).
+  int ksplit;
+  float* ws;
+  uint32_t* wsflag;
 };
 
 constexpr int kGroupM = 8;

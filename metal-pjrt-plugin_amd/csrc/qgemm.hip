@@ -19,7 +19,6 @@
 #include <string>
 
 #include "gemm_common.h"
-#include "qgemm_dma.h"
 #include "qk_device.h"
 #include "qk_internal.h"
 
@@ -248,69 +247,6 @@ struct QuantFastB {
   }
 };
 
-// The register-dequantizing DMA kernel (qgemm_dma.h) for int4 u32x8
-// codes: any M, N a multiple of 128, K of 512, group 64, bf16 scales and
-// offsets, 16-byte aligned x, codes, scales and offsets; false when it does
-// not apply. Tile: 256 x 256 (eight waves of 256 x 32, three A stages) or
-// 256 x 128 (four waves of 256 x 32, four stages), the fewest rounds of
-// one tile per CU weighted by a round's cost relative to 256 x 256
-// (measured on MI355X at 2048 x 12288 x 4096: 0.74).
-template <typename T, int PACK>
-bool LaunchDmaQ(GemmArgs g, int m, int n, hipStream_t stream, qk_status* st) {
-  if constexpr (PACK != QK_PACK_U32X8) {
-    return false;
-  } else {
-    if (m <= 0 || g.k % 512 != 0 || g.k == 0 || g.qgroup != 64 ||
-        g.qsdt != QK_BF16 || (g.qhas_bias && g.qbdt != QK_BF16) ||
-        n % 128 != 0 ||
-        static_cast<int64_t>(n) * g.qrow_bytes >= (int64_t{1} << 31) ||
-        static_cast<int64_t>(n) * (g.k / 64) * 2 >= (int64_t{1} << 31) ||
-        (static_cast<int64_t>(m) + 256) * g.k * 2 >= (int64_t{1} << 31) ||
-        reinterpret_cast<uintptr_t>(g.a) % 16 != 0 ||
-        reinterpret_cast<uintptr_t>(g.b) % 16 != 0 ||
-        reinterpret_cast<uintptr_t>(g.qscale) % 16 != 0 ||
-        (g.qhas_bias && reinterpret_cast<uintptr_t>(g.qbias) % 16 != 0))
-      return false;
-    const int cus = DeviceComputeUnits();
-    // QK_QGEMM_DMA_BN=128|256 forces the tile width (tuning).
-    static const int forced = [] {
-      const char* v = std::getenv("QK_QGEMM_DMA_BN");
-      return v == nullptr ? 0 : std::atoi(v);
-    }();
-    const long long mt = (m + 255) / 256;
-    const struct { int bn; double cost; } cand[] = {{256, 1.0}, {128, 0.74}};
-    int bn = 0;
-    double best = 1e30;
-    for (const auto& c : cand) {
-      if (n % c.bn != 0) continue;
-      const long long tiles = mt * (n / c.bn);
-      const double r = c.cost * static_cast<double>((tiles + cus - 1) / cus);
-      if (forced == c.bn) {
-        bn = c.bn;
-        break;
-      }
-      if (r < best) best = r, bn = c.bn;
-    }
-    g.tiles_m = static_cast<int>(mt);
-    g.tiles_n = n / bn;
-    const dim3 grid(g.tiles_m * g.tiles_n);
-    const bool mc = m % 256 != 0;
-    if (bn == 256) {
-      if (mc)
-        qgemm_dma_kernel<T, 256, 1, 1, 3, true><<<grid, 512, 0, stream>>>(g);
-      else
-        qgemm_dma_kernel<T, 256, 1, 1, 3, false><<<grid, 512, 0, stream>>>(g);
-    } else {
-      if (mc)
-        qgemm_dma_kernel<T, 128, 1, 1, 4, true><<<grid, 256, 0, stream>>>(g);
-      else
-        qgemm_dma_kernel<T, 128, 1, 1, 4, false><<<grid, 256, 0, stream>>>(g);
-    }
-    *st = PostLaunch("qgemm_dma");
-    return true;
-  }
-}
-
 // The interior-tile kernel for any M, N a multiple of 128, group 64, bf16
 // scales/offsets; false when it does not apply. Eight waves; tiles of
 // 256 x 256, 256 x 128 or 128 x 128 (two workgroups per CU); the last M
@@ -391,7 +327,6 @@ qk_status LaunchTileQ(const GemmArgs& g, hipStream_t stream) {
 template <typename T, int PACK>
 qk_status LaunchQ(const GemmArgs& g0, int m, int n, hipStream_t stream) {
   qk_status st = QK_OK;
-  if (LaunchDmaQ<T, PACK>(g0, m, n, stream, &st)) return st;
   if (LaunchFastQ<T, PACK>(g0, m, n, stream, &st)) return st;
   GemmArgs g = g0;
   const int cus = DeviceComputeUnits();

@@ -1,5 +1,6 @@
-// Quantized prefill GEMM for gfx950: y = x @ w^T with int4 (u32x8) weight
-// codes dequantized in registers, straight into the MFMA B fragments.
+// Quantized prefill GEMM for gfx950: y = x @ w^T with int4 (u32x8) or int8
+// (u8 affine, s8 symmetric) weight codes dequantized in registers, straight
+// into the MFMA B fragments.
 //
 // Replaces the reference's path for rows beyond ROWS_MAX (4) in linear()
 // (examples/llm/qwen3.py:218-230): w = dequantize(w, x.dtype)
@@ -10,24 +11,30 @@
 // of x with the dequantized weights, accumulated in f32.
 //
 // Layout and schedule (the interior-tile scheme of gemm_dma.h):
-//  - 256 x BN tiles, K tiles of 64 (one quantization group); every operand
+//  - BM x BN tiles (BM 256 or 128), K tiles of 64 (one quantization
+//    group); every operand
 //    reaches LDS by DMA (`buffer_load ... lds`), issued evenly by the
 //    waves, in pieces of whole 64- or 128-byte lines (a DMA instruction
 //    that touches many lines for few bytes each is what limits a CU's
 //    fetch rate, more than the bytes):
-//    * A (x rows): S stages (three or four) of 256 rows x 128 bytes, one
+//    * A (x rows): S stages (three or four) of BM rows x 128 bytes, one
 //      per K tile; 16-byte chunk c of row r in slot c ^ ((r >> 1) & 7).
-//    * Codes: blocks of two K tiles, 64 bytes (128 codes) per weight row,
-//      S / 2 + 1 blocks resident; chunk c of row n in slot c ^ ((n >> 2) & 3).
+//      When the BM / 8 instructions of a stage do not split evenly over
+//      the waves, the waves short of one issue an out-of-range DMA (zeros,
+//      no memory access) into a spare 1 KB, so every wave's memory counter
+//      counts the same number per stage.
+//    * Codes: blocks of two K tiles, 64 bytes (int4, 128 codes) or 128
+//      bytes (int8) per weight row, S / 2 + 1 blocks resident; chunk c of
+//      row n in slot c ^ ((n >> 2) & 3) (int4) or c ^ (n & 7) (int8).
 //    * Scales and offsets: blocks of eight K tiles, 16 bytes (eight bf16
 //      groups) per row each, two blocks resident.
 //    A code (scale) block is fetched with the DMA of its first K tile.
-//  - Waves WM x WN, each 256 / WM rows x 32 FN columns
+//  - Waves WM x WN, each BM / WM rows x 32 FN columns
 //    (v_mfma_f32_32x32x16): FM = 8 / WM A fragments (16-byte LDS reads) and
 //    FN B fragments per K step of 16. A B fragment is lane l's column
-//    n = l % 32 at K 8 (l / 32) .. + 7: one 32-bit LDS read of that row's
-//    code word, its nibbles split into bytes and converted to f32, one fma
-//    each with the row's group scale and offset, and packed to T. Each B
+//    n = l % 32 at K 8 (l / 32) .. + 7: that row's code word (int4) or
+//    two (int8), the codes converted to f32, one fma each with the row's
+//    group scale and offset, and packed to T. Each B
 //    fragment feeds FM MFMAs: with WM = 1 the dequantizing VALU work is a
 //    third of the MFMA time and no column is dequantized twice in a CU.
 //  - One barrier per K tile, as in gemm_dma.h: each wave waits for its own
@@ -35,6 +42,14 @@
 //    kt + S into the freed stage is issued (with the code or scale block
 //    it starts), then the MFMAs of step 3 with the fragment reads of the
 //    next tile's step 0.
+//  - Split K (ksplit > 1, for grids that would otherwise leave CUs idle):
+//    workgroup (tile, z) takes K tiles z G / ksplit .. (z + 1) G / ksplit
+//    (whole scale blocks), writes its f32 partial tile to the workspace
+//    and counts itself in on the tile's arrival counter (a device-scope
+//    atomic, once its stores have completed). The last to arrive sums the ksplit
+//    partials in the order z = 0, 1, ... (its own from registers), so the
+//    result does not depend on the arrival order, resets the counter to
+//    zero for the next launch and stores the tile with the epilogue.
 #pragma once
 
 #include "gemm_common.h"
@@ -42,15 +57,19 @@
 namespace qk {
 namespace {
 
-template <typename T, int BN, int WM, int FN, int S>
+template <typename T, int PACK, int BM_, int BN, int WM, int FN, int S>
 struct QDma {
-  static constexpr int BM = 256, BK = 64, WTM = BM / WM, FM = WTM / 32;
+  static constexpr bool kInt4 = PACK == QK_PACK_U32X8;
+  static constexpr int BM = BM_, BK = 64, WTM = BM / WM, FM = WTM / 32;
   static constexpr int WTN = 32 * FN, WN = BN / WTN, NW = WM * WN;
   static constexpr int NT = NW * 64;
   static constexpr int CB = 2;           // K tiles per code block
   static constexpr int SBK = 8;          // K tiles per scale block
   static constexpr int kA = BM * 128;    // A stage bytes
-  static constexpr int kCRow = 32 * CB;  // code bytes per row per block
+  static constexpr int kCT = kInt4 ? 32 : 64;  // code bytes per row, K tile
+  static constexpr int kCRow = kCT * CB; // code bytes per row per block
+  static constexpr int kCLanes = kCRow / 16;   // lanes per row in a DMA
+  static constexpr int kCRows = 64 / kCLanes;  // rows per code DMA
   static constexpr int kCB = BN * kCRow; // code block bytes
   static constexpr int kSB = BN * 16;    // scale (offset) block bytes
   // Code blocks resident: block c is fetched at tile 2 c - S into the
@@ -58,15 +77,17 @@ struct QDma {
   // 2 (c - NCB) + 1, at the end of tile 2 (c - NCB)) must come before that
   // tile's barrier: NCB > S / 2. Scale blocks: 8 NSB > S + 6, so two.
   static constexpr int NCB = S / 2 + 1;
+  static constexpr int kAI = BM / 8;        // 1 KB A DMA instructions
+  static constexpr int kNA = (kAI + NW - 1) / NW;  // per wave
+  static constexpr bool kPad = kAI % NW != 0;
   static constexpr int kCOff = S * kA;
   static constexpr int kSOff = kCOff + NCB * kCB;
-  static constexpr int kBytes = kSOff + 4 * kSB;  // 2 blocks x (s, b)
-  static constexpr int kAI = BM / 8;        // 1 KB A DMA instructions
+  static constexpr int kDOff = kSOff + 4 * kSB;  // 2 blocks x (s, b)
+  static constexpr int kBytes = kDOff + (kPad ? 1024 : 0);
   static constexpr int kCI = kCB / 1024;    // code block instructions
   static constexpr int kSI = kSB / 1024;    // scale (offset) block instr.
-  static constexpr int kNA = kAI / NW;      // A instructions per wave
   static_assert(BN % WTN == 0 && BN % 64 == 0, "tile split");
-  static_assert(kAI % NW == 0, "every wave issues the same A DMAs");
+  static_assert(BM % (32 * WM) == 0, "wave rows");
   static_assert(kBytes <= 160 * 1024, "LDS");
 };
 
@@ -95,30 +116,88 @@ __device__ __forceinline__ typename Frag<T>::type DequantWord(uint32_t w,
   return __builtin_bit_cast(typename Frag<T>::type, out);
 }
 
-// MC: M need not be a multiple of 256 (A rows past M read zeros through
+// Eight int8 codes (bytes 0..3 of w0, then of w1, in K order) as
+// T(f32(q) * s + b); u8 codes convert with one v_cvt_f32_ubyteN each, s8
+// codes are sign-extended first.
+template <typename T, int PACK>
+__device__ __forceinline__ typename Frag<T>::type DequantBytes(uint32_t w0,
+                                                               uint32_t w1,
+                                                               float s,
+                                                               float b) {
+  typedef T T2 __attribute__((ext_vector_type(2)));
+  u32x4 out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t w = e < 2 ? w0 : w1;
+    const uint32_t b0 = (w >> (16 * (e & 1))) & 0xFFu;
+    const uint32_t b1 = (w >> (16 * (e & 1) + 8)) & 0xFFu;
+    float q0, q1;
+    if constexpr (PACK == QK_PACK_S8_SYM) {
+      q0 = static_cast<float>(static_cast<int8_t>(b0));
+      q1 = static_cast<float>(static_cast<int8_t>(b1));
+    } else {
+      q0 = static_cast<float>(b0);
+      q1 = static_cast<float>(b1);
+    }
+    const T2 p = {from_f32<T>(fmaf(q0, s, b)), from_f32<T>(fmaf(q1, s, b))};
+    out[e] = __builtin_bit_cast(uint32_t, p);
+  }
+  return __builtin_bit_cast(typename Frag<T>::type, out);
+}
+
+// A lane's codes of one weight row for one K tile: 16 bytes (int4) or 32
+// (int8), K 32 (l / 32) .. + 31 of the tile; K step s takes word s (int4)
+// or words 2 s and 2 s + 1 (int8).
+template <int PACK>
+struct QTileCodes {
+  static constexpr int kN = PACK == QK_PACK_U32X8 ? 1 : 2;
+  u32x4 c[kN];
+  template <typename T>
+  __device__ __forceinline__ typename Frag<T>::type dq(int s, float sc,
+                                                      float bi) const {
+    if constexpr (PACK == QK_PACK_U32X8)
+      return DequantWord<T>(c[0][s], sc, bi);
+    else
+      return DequantBytes<T, PACK>(c[kN - 1 > 0 ? s >> 1 : 0][2 * (s & 1)],
+                                   c[kN - 1 > 0 ? s >> 1 : 0][2 * (s & 1) + 1],
+                                   sc, bi);
+  }
+};
+
+// MC: M need not be a multiple of BM (A rows past M read zeros through
 // the descriptor's extent; their outputs are not stored). K is a multiple
-// of 512 (whole scale blocks).
-template <typename T, int BN, int WM, int FN, int S, bool MC>
-__global__ __launch_bounds__((QDma<T, BN, WM, FN, S>::NT)) void qgemm_dma_kernel(
-    GemmArgs g) {
-  using C = QDma<T, BN, WM, FN, S>;
+// of 512 (whole scale blocks), and so is every split's K range.
+template <typename T, int PACK, int BM, int BN, int WM, int FN, int S,
+          bool MC>
+__global__ __launch_bounds__((QDma<T, PACK, BM, BN, WM, FN, S>::NT)) void
+qgemm_dma_kernel(GemmArgs g) {
+  using C = QDma<T, PACK, BM, BN, WM, FN, S>;
   constexpr int FM = C::FM, WN = C::WN, NW = C::NW;
   using F = typename Frag<T>::type;
+  using Codes = QTileCodes<PACK>;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::kBytes];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
-  const int nwg = g.tiles_m * g.tiles_n;
+  const int ntiles = g.tiles_m * g.tiles_n;
+  const int splits = g.ksplit;
+  const int nwg = ntiles * splits;
   int bid = blockIdx.x;
   if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+  // Consecutive workgroups (one XCD's share) take one K range of
+  // neighbouring tiles.
+  const int z = bid / ntiles;
+  const int tile = bid - z * ntiles;
   const int group_span = kGroupM * g.tiles_n;
-  const int first_m = (bid / group_span) * kGroupM;
+  const int first_m = (tile / group_span) * kGroupM;
   const int gsz = min(g.tiles_m - first_m, kGroupM);
-  const int tm = first_m + (bid % group_span) % gsz;
-  const int tn = (bid % group_span) / gsz;
-  const int m0 = tm * C::BM, n0 = tn * BN;
+  const int tm = first_m + (tile % group_span) % gsz;
+  const int tn = (tile % group_span) / gsz;
+  const int m0 = tm * BM, n0 = tn * BN;
   const int G = g.k / 64;  // groups (K tiles) per weight row
+  const int kper = G / splits;
+  const int kbeg = z * kper, kend = kbeg + kper;
 
   DmaRsrc ra, rc, rs, rb;
   ra.make(g.a, static_cast<long long>(g.m) * g.lda * sizeof(T));
@@ -128,21 +207,25 @@ __global__ __launch_bounds__((QDma<T, BN, WM, FN, S>::NT)) void qgemm_dma_kernel
   rb.make(g.qbias, g.qhas_bias ? static_cast<long long>(g.n) * G * 2 : 0);
 
   // The DMA of K tile kt: its A stage (instruction d fills rows 8 d ..
-  // 8 d + 7), then the code block it starts (instruction j: rows 16 j ..
-  // 16 j + 15, four 16-byte chunks each) and the scale and offset block it
-  // starts (instruction j: 64 rows, 16 bytes each). Wave w takes every
-  // NW-th instruction of each kind. `a_st` is the stage's LDS address.
+  // 8 d + 7), then the code block it starts (instruction j: kCRows rows,
+  // kCLanes 16-byte chunks each) and the scale and offset block it starts
+  // (instruction j: 64 rows, 16 bytes each). Wave w takes every NW-th
+  // instruction of each kind. `a_st` is the stage's LDS address.
   auto issue = [&](unsigned char* a_st, int kt) {
     const int k0 = kt * 64;
 #pragma unroll
     for (int t = 0; t < C::kNA; ++t) {
       const int d = wave + NW * t;
-      const int row = 8 * d + lane / 8;
-      const int chunk = (lane % 8) ^ ((row >> 1) & 7);
-      ra.dma(a_st + d * 1024,
-             ((m0 + row) * g.lda + k0 + chunk * 8) *
-                 static_cast<int>(sizeof(T)),
-             0);
+      if (C::kPad && d >= C::kAI) {
+        ra.dma(smem + C::kDOff, 0x7FFF0000, 0);  // zeros, counted alike
+      } else {
+        const int row = 8 * d + lane / 8;
+        const int chunk = (lane % 8) ^ ((row >> 1) & 7);
+        ra.dma(a_st + d * 1024,
+               ((m0 + row) * g.lda + k0 + chunk * 8) *
+                   static_cast<int>(sizeof(T)),
+               0);
+      }
     }
     if (kt % C::CB == 0) {
       unsigned char* cb =
@@ -151,10 +234,11 @@ __global__ __launch_bounds__((QDma<T, BN, WM, FN, S>::NT)) void qgemm_dma_kernel
       for (int t = 0; t < (C::kCI + NW - 1) / NW; ++t) {
         const int j = wave + NW * t;
         if (j >= C::kCI) break;
-        const int row = 16 * j + lane / 4;
-        const int chunk = (lane % 4) ^ ((row >> 2) & 3);
+        const int row = C::kCRows * j + lane / C::kCLanes;
+        const int chunk =
+            (lane % C::kCLanes) ^ (C::kInt4 ? (row >> 2) & 3 : row & 7);
         rc.dma(cb + j * 1024,
-               (n0 + row) * g.qrow_bytes + k0 / 2 + chunk * 16, 0);
+               (n0 + row) * g.qrow_bytes + kt * C::kCT + chunk * 16, 0);
       }
     }
     if (kt % C::SBK == 0) {
@@ -177,8 +261,8 @@ __global__ __launch_bounds__((QDma<T, BN, WM, FN, S>::NT)) void qgemm_dma_kernel
   // Within a K tile the K steps are taken in a permuted order (the sum
   // over K does not depend on it): K step s gives lane half h = l / 32 the
   // eight K elements 32 h + 8 s .. + 7, so over the four steps a lane's B
-  // elements of a row are one 16-byte chunk of codes (32 h / 2 bytes on),
-  // read once per tile.
+  // elements of a row are one contiguous run of codes (16 bytes of int4,
+  // 32 of int8), read once per tile.
   auto frag_a = [&](const unsigned char* st, int i, int s) {
     const int r = wm * C::WTM + i * 32 + (lane & 31);
     const int c = 4 * (lane >> 5) + s;
@@ -198,14 +282,26 @@ __global__ __launch_bounds__((QDma<T, BN, WM, FN, S>::NT)) void qgemm_dma_kernel
                               *reinterpret_cast<const uint16_t*>(p + C::kSB))
                           << 16);
   };
-  // This lane's 16-byte code chunk of fragment j's column in K tile kt
-  // (chunk 2 (kt % 2) + l / 32 of the row in code block kt / 2).
+  // This lane's codes of fragment j's column in K tile kt: 16-byte chunk
+  // 2 (kt % 2) + l / 32 of the row's int4 block, or chunks
+  // 4 (kt % 2) + 2 (l / 32) and the next of its int8 block.
   auto codes = [&](int j, int kt) {
     const int n = wn * C::WTN + 32 * j + (lane & 31);
-    const int c = (kt % C::CB) * 2 + (lane >> 5);
-    return *reinterpret_cast<const u32x4*>(
-        smem + C::kCOff + ((kt / C::CB) % C::NCB) * C::kCB + n * C::kCRow +
-        ((c ^ ((n >> 2) & 3)) << 4));
+    const unsigned char* row =
+        smem + C::kCOff + ((kt / C::CB) % C::NCB) * C::kCB + n * C::kCRow;
+    Codes cw;
+    if constexpr (C::kInt4) {
+      const int c = (kt % C::CB) * 2 + (lane >> 5);
+      cw.c[0] = *reinterpret_cast<const u32x4*>(row +
+                                                ((c ^ ((n >> 2) & 3)) << 4));
+    } else {
+      const int c = (kt % C::CB) * 4 + 2 * (lane >> 5);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        cw.c[h] = *reinterpret_cast<const u32x4*>(
+            row + (((c + h) ^ (n & 7)) << 4));
+    }
+    return cw;
   };
   f32x16 acc[FM][FN];
 #pragma unroll
@@ -215,33 +311,33 @@ __global__ __launch_bounds__((QDma<T, BN, WM, FN, S>::NT)) void qgemm_dma_kernel
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int ktiles = G;  // >= 8
   auto stage = [&](int i) { return smem + i * C::kA; };
 #pragma unroll
-  for (int t = 0; t < S; ++t) issue(stage(t), t);
-  // Tile 0 (with its blocks) has landed: the A DMAs of tiles 1 .. S - 1
-  // may still be in flight (the waves' block DMAs, issued with some tiles
-  // and not others, only add to what is waited for, never to what is left
-  // outstanding).
+  for (int t = 0; t < S; ++t) issue(stage(t), kbeg + t);
+  // Tile kbeg (with its blocks) has landed: the A DMAs of the next S - 1
+  // tiles may still be in flight (the waves' block DMAs, issued with some
+  // tiles and not others, only add to what is waited for, never to what is
+  // left outstanding).
   __builtin_amdgcn_s_waitcnt(VmcntImm((S - 1) * C::kNA));
   __syncthreads();
   F fa[2][FM], fb[2][FN];
   float scl[FN], bil[FN];
-  u32x4 cw[FN];  // code chunks of the current tile
+  Codes cw[FN];  // code runs of the current tile
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
-    sb(j, 0, &scl[j], &bil[j]);
-    cw[j] = codes(j, 0);
+    sb(j, kbeg, &scl[j], &bil[j]);
+    cw[j] = codes(j, kbeg);
   }
 #pragma unroll
   for (int i = 0; i < FM; ++i) fa[0][i] = frag_a(stage(0), i, 0);
 #pragma unroll
-  for (int j = 0; j < FN; ++j) fb[0][j] = DequantWord<T>(cw[j][0], scl[j], bil[j]);
+  for (int j = 0; j < FN; ++j)
+    fb[0][j] = cw[j].template dq<T>(0, scl[j], bil[j]);
 
   constexpr int kReads = FM;
-  // K tile kt from A stage SLOT = kt % S; tile kt + 1 is in stage
+  // K tile kt from A stage SLOT = (kt - kbeg) % S; tile kt + 1 is in stage
   // (SLOT + 1) % S; after the barrier tile kt + S goes into stage SLOT.
-  auto tile = [&](int kt, auto slot_c) {
+  auto tile_step = [&](int kt, auto slot_c) {
     constexpr int SLOT = decltype(slot_c)::value;
     unsigned char* cs = stage(SLOT);
     unsigned char* ns = stage((SLOT + 1) % S);
@@ -252,7 +348,7 @@ __global__ __launch_bounds__((QDma<T, BN, WM, FN, S>::NT)) void qgemm_dma_kernel
       for (int i = 0; i < FM; ++i) fa[fn][i] = frag_a(cs, i, s + 1);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        fb[fn][j] = DequantWord<T>(cw[j][s + 1], scl[j], bil[j]);
+        fb[fn][j] = cw[j].template dq<T>(s + 1, scl[j], bil[j]);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -270,7 +366,7 @@ __global__ __launch_bounds__((QDma<T, BN, WM, FN, S>::NT)) void qgemm_dma_kernel
     __syncthreads();
     // (Past the last tile the last one is fetched again into the free
     // stage, so that every wait above counts the same DMAs.)
-    issue(cs, min(kt + S, ktiles - 1));
+    issue(cs, min(kt + S, kend - 1));
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       sb(j, kt + 1, &scl[j], &bil[j]);
@@ -284,28 +380,124 @@ __global__ __launch_bounds__((QDma<T, BN, WM, FN, S>::NT)) void qgemm_dma_kernel
     }
 #pragma unroll
     for (int j = 0; j < FN; ++j)
-      fb[0][j] = DequantWord<T>(cw[j][0], scl[j], bil[j]);
+      fb[0][j] = cw[j].template dq<T>(0, scl[j], bil[j]);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
   static_assert(S == 3 || S == 4, "unrolled for three or four stages");
-  int kt = 0;
-  for (; kt + S <= ktiles; kt += S) {
-    tile(kt, I0{});
-    tile(kt + 1, I1{});
-    tile(kt + 2, I2{});
-    if constexpr (S == 4) tile(kt + 3, I3{});
+  int kt = kbeg;
+  for (; kt + S <= kend; kt += S) {
+    tile_step(kt, I0{});
+    tile_step(kt + 1, I1{});
+    tile_step(kt + 2, I2{});
+    if constexpr (S == 4) tile_step(kt + 3, I3{});
   }
-  if (kt < ktiles) tile(kt, I0{});
-  if (kt + 1 < ktiles) tile(kt + 1, I1{});
+  if (kt < kend) tile_step(kt, I0{});
+  if (kt + 1 < kend) tile_step(kt + 1, I1{});
   if constexpr (S == 4) {
-    if (kt + 2 < ktiles) tile(kt + 2, I2{});
+    if (kt + 2 < kend) tile_step(kt + 2, I2{});
   }
   // No DMA may still be writing this workgroup's LDS when it ends.
   __builtin_amdgcn_s_waitcnt(VmcntImm(0));
-  store_direct<T, C::BM, BN, WM, WN, MC>(g, acc, m0, n0, 0, lane, wm, wn);
+  if (splits > 1) {
+    // Partial tile of (tile, z): value r of fragment (i, j) of thread t at
+    // float ((i FN + j) 16 + r) NT + t (coalesced stores and loads). The
+    // partials and the counter are accessed as device-scope relaxed atomics
+    // (coherent loads and stores past the non-coherent caches), and the
+    // order "partial, then arrival" comes from waiting for the stores to
+    // complete before the counter is incremented. A device-scope fence
+    // would do the same by writing back and invalidating the whole L2,
+    // which costs the other workgroups their cached x and codes.
+    constexpr int kPer = FM * FN * 16;
+    // Partials through a buffer descriptor with the sc1 cache policy
+    // (device-coherent: write-through stores, loads that miss stale
+    // lines), 16 bytes per lane: four values r = 4 u .. 4 u + 3 of
+    // fragment q = i FN + j of thread t at float4 (q 4 + u) NT + t.
+    const long long wsbytes = static_cast<long long>(ntiles) * splits * kPer *
+                              C::NT * 4;
+    const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(
+        g.ws, (short)0,
+        static_cast<int>(wsbytes < 0x7FFFFFFFll ? wsbytes : 0x7FFFFFFFll),
+        0x00020000);
+    constexpr int kSc1 = 16;
+    auto part_off = [&](int zz, int q, int u) {
+      return ((((tile * splits + zz) * kPer / 4) + q * 4 + u) * C::NT + tid) *
+             16;
+    };
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          f32x4 v = {acc[i][j][4 * u], acc[i][j][4 * u + 1],
+                     acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(u32x4, v), wsr, part_off(z, i * FN + j, u),
+              0, kSc1);
+        }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    uint32_t* const flag = reinterpret_cast<uint32_t*>(smem);
+    if (tid == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(
+          g.wsflag + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t last = old + 1 == static_cast<uint32_t>(splits);
+      if (last)
+        __hip_atomic_store(g.wsflag + tile, 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      *flag = last;
+    }
+    __syncthreads();
+    if (*flag == 0) return;
+    // The sum in the order z = 0, 1, ... (the result does not depend on
+    // which workgroup arrived last), four fragments at a time: the 64
+    // loads of one partial's share are all issued before they are added,
+    // so each partial costs one memory round trip.
+    constexpr int kFrags = FM * FN;
+    constexpr int kChunk = kFrags < 4 ? kFrags : 4;
+#pragma unroll
+    for (int q0 = 0; q0 < kFrags; q0 += kChunk) {
+      float t[kChunk][16];
+#pragma unroll
+      for (int q = 0; q < kChunk; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) t[q][r] = 0.f;
+      for (int zz = 0; zz < splits; ++zz) {
+        float v[kChunk][16];
+        if (zz == z) {
+#pragma unroll
+          for (int q = 0; q < kChunk; ++q)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              v[q][r] = acc[(q0 + q) / FN][(q0 + q) % FN][r];
+        } else {
+#pragma unroll
+          for (int q = 0; q < kChunk; ++q)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const f32x4 l = __builtin_bit_cast(
+                  f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                             wsr, part_off(zz, q0 + q, u), 0, kSc1));
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[q][4 * u + e] = l[e];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < kChunk; ++q)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) t[q][r] += v[q][r];
+      }
+#pragma unroll
+      for (int q = 0; q < kChunk; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          acc[(q0 + q) / FN][(q0 + q) % FN][r] = t[q][r];
+    }
+  }
+  store_direct<T, BM, BN, WM, WN, MC>(g, acc, m0, n0, 0, lane, wm, wn);
 }
 
 }  // namespace

@@ -13,6 +13,7 @@
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "qk_internal.h"
 
@@ -131,6 +132,56 @@ int DeviceComputeUnits() {
     cached[dev] = cus;
   }
   return cached[dev];
+}
+
+bool StreamWorkspace(hipStream_t stream, size_t bytes, float** ws,
+                     uint32_t** flags) {
+  struct Entry {
+    int dev;
+    hipStream_t stream;
+    void* p;
+    size_t bytes;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> table;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  const size_t need = kWsFlagBytes + ((bytes + 255) / 256) * 256;
+  std::lock_guard<std::mutex> lock(mu);
+  Entry* e = nullptr;
+  for (auto& t : table)
+    if (t.dev == dev && t.stream == stream) e = &t;
+  if (e != nullptr && e->bytes >= need) {
+    *flags = static_cast<uint32_t*>(e->p);
+    *ws = reinterpret_cast<float*>(static_cast<char*>(e->p) + kWsFlagBytes);
+    return true;
+  }
+  // Growing allocates: not while the stream is captured.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess ||
+      cap != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return false;
+  }
+  const size_t size = std::max<size_t>(need, size_t{32} << 20);
+  // A smaller buffer being replaced is not freed: launches still queued
+  // on the stream, and graphs captured from it, keep using it.
+  void* p = nullptr;
+  if (hipMalloc(&p, size) != hipSuccess ||
+      hipMemset(p, 0, kWsFlagBytes) != hipSuccess) {
+    if (p != nullptr) (void)hipFree(p);
+    (void)hipGetLastError();
+    return false;
+  }
+  if (e == nullptr) {
+    table.push_back(Entry{dev, stream, p, size});
+  } else {
+    e->p = p;
+    e->bytes = size;
+  }
+  *flags = static_cast<uint32_t*>(p);
+  *ws = reinterpret_cast<float*>(static_cast<char*>(p) + kWsFlagBytes);
+  return true;
 }
 
 int ResidentBlocks(const void* kernel, int block, size_t lds) {

@@ -43,6 +43,20 @@ uint32_t ReadDeviceStatusWords(bool clear);
 // Compute units of the current device (cached per device).
 int DeviceComputeUnits();
 
+// Split-K workspace owned by the library, one per (device, stream): *ws
+// takes at least `bytes` of f32 partials, *flags kWsFlagBytes / 4 arrival
+// counters (zero between launches). Grown on demand by a new allocation
+// (the old one stays valid for launches already queued and for graphs
+// captured from the stream), never freed before the process ends.
+// Launches on one stream run in order, so they never use it concurrently;
+// a captured graph keeps its capture stream's buffer, so its replays must
+// not overlap other launches on that stream. False while the stream is
+// being captured and the workspace is too small, or when allocation
+// fails: the caller then takes a path without split K.
+constexpr size_t kWsFlagBytes = 64 * 1024;
+bool StreamWorkspace(hipStream_t stream, size_t bytes, float** ws,
+                     uint32_t** flags);
+
 // Workgroups of `kernel` one CU keeps resident with this block size and
 // dynamic LDS (cached; at least 1).
 int ResidentBlocks(const void* kernel, int block, size_t lds);
@@ -126,6 +140,11 @@ qk_status LaunchQMid(const QuantProblem& p, hipStream_t stream);
 
 // Dequantizing MFMA GEMM (qgemm.hip) for more than four rows of x.
 bool QGemmApplies(const QuantProblem& p);
+// The register-dequantizing GEMM (qgemm_dma.hip): int4 u32x8 / u8 / s8,
+// group 64, bf16 scales, K a multiple of 512, N of 128, 16-byte aligned
+// operands; tile and K split chosen per problem.
+bool QGemmDmaApplies(const QuantProblem& p);
+qk_status LaunchQGemmDma(const QuantProblem& p, hipStream_t stream);
 qk_status LaunchQGemm(const QuantProblem& p, hipStream_t stream);
 qk_status LaunchDequantize(const QuantProblem& p, hipStream_t stream);
 

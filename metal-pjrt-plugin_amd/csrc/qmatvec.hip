@@ -1428,11 +1428,22 @@ qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream) {
   // Beyond four rows the reference's linear() (ROWS_MAX = 4,
   // examples/llm/qwen3.py:215-230) dequantizes to x's type and multiplies.
   // Up to 32 rows (int4 and int8) stream through MFMA with the codes kept
-  // factored per group (qskinny.hip); up to 128 rows dequantize
-  // in registers with K split over the waves of a workgroup (qmid.hip);
-  // otherwise dequantize and multiply in one fused MFMA GEMM (qgemm.hip).
+  // factored per group (qskinny.hip); 33..64 rows dequantize in registers
+  // with K split over the waves of a workgroup (qmid.hip); beyond, and
+  // where qmid does not apply, dequantize in registers into the MFMA
+  // operands of one GEMM (qgemm_dma.hip, K split over workgroups when
+  // the tiles alone would not fill the CUs; other packings qgemm.hip).
+  // QK_QGEMM_DMA_MIN_M: fewest rows for the register-dequantizing GEMM
+  // (tuning; read at every call).
+  const char* dmv = std::getenv("QK_QGEMM_DMA_MIN_M");
+  const int dma_min_m = dmv == nullptr ? 33 : std::atoi(dmv);
   if (m > 4 && QSkinnyApplies(p)) return LaunchQSkinny(p, stream);
-  if (m > 4 && QMidApplies(p)) return LaunchQMid(p, stream);
+  // 33..64 rows: the K-split dequantizing kernel where it applies (int4
+  // 12288 x 4096: 21 / 24 us at M = 33 / 64 against 31 for the GEMM).
+  const bool mid = m > 4 && QMidApplies(p);
+  if (m >= dma_min_m && (m > 64 || !mid) && QGemmDmaApplies(p))
+    return LaunchQGemmDma(p, stream);
+  if (mid) return LaunchQMid(p, stream);
   if (m > 4 && QGemmApplies(p)) return LaunchQGemm(p, stream);
   if (m <= 4) {
     const int cus = DeviceComputeUnits();
