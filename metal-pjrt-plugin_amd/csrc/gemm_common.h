@@ -45,6 +45,8 @@ struct GemmArgs {
   // Split K (qgemm_dma.h): K ranges per tile (1: none), the f32 partial
   // tiles and the per-tile arrival counters (zero between launches).
   int ksplit;
+  // M tiles per tile group of the workgroup order (qgemm_dma.h; 0: kGroupM)
+  int group_m;
   float* ws;
   uint32_t* wsflag;
 };

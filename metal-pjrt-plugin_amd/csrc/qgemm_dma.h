@@ -181,23 +181,25 @@ qgemm_dma_kernel(GemmArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int ntiles = g.tiles_m * g.tiles_n;
+  const int G = g.k / 64;  // groups (K tiles) per weight row
   const int splits = g.ksplit;
   const int nwg = ntiles * splits;
-  int bid = blockIdx.x;
-  if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
-  // Consecutive workgroups (one XCD's share) take one K range of
-  // neighbouring tiles.
-  const int z = bid / ntiles;
-  const int tile = bid - z * ntiles;
-  const int group_span = kGroupM * g.tiles_n;
-  const int first_m = (tile / group_span) * kGroupM;
-  const int gsz = min(g.tiles_m - first_m, kGroupM);
-  const int tm = first_m + (tile % group_span) % gsz;
-  const int tn = (tile % group_span) / gsz;
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int G = g.k / 64;  // groups (K tiles) per weight row
-  const int kper = G / splits;
-  const int kbeg = z * kper, kend = kbeg + kper;
+  int w = blockIdx.x;
+  if ((nwg & 7) == 0) w = (w & 7) * (nwg >> 3) + (w >> 3);
+  // Workgroup w = z ntiles + tile takes K range z of the tile, so one
+  // XCD's share (consecutive w) takes one K range of neighbouring tiles.
+  const int z = w / ntiles;
+  const int tile = w - z * ntiles;
+  const int kbeg = z * (G / splits), kend = kbeg + G / splits;
+  int m0, n0;
+  {
+    const int gm = g.group_m > 0 ? g.group_m : kGroupM;
+    const int group_span = gm * g.tiles_n;
+    const int first_m = (tile / group_span) * gm;
+    const int gsz = min(g.tiles_m - first_m, gm);
+    m0 = (first_m + (tile % group_span) % gsz) * BM;
+    n0 = ((tile % group_span) / gsz) * BN;
+  }
 
   DmaRsrc ra, rc, rs, rb;
   ra.make(g.a, static_cast<long long>(g.m) * g.lda * sizeof(T));
@@ -401,30 +403,28 @@ qgemm_dma_kernel(GemmArgs g) {
   }
   // No DMA may still be writing this workgroup's LDS when it ends.
   __builtin_amdgcn_s_waitcnt(VmcntImm(0));
-  if (splits > 1) {
-    // Partial tile of (tile, z): value r of fragment (i, j) of thread t at
-    // float ((i FN + j) 16 + r) NT + t (coalesced stores and loads). The
-    // partials and the counter are accessed as device-scope relaxed atomics
-    // (coherent loads and stores past the non-coherent caches), and the
-    // order "partial, then arrival" comes from waiting for the stores to
-    // complete before the counter is incremented. A device-scope fence
-    // would do the same by writing back and invalidating the whole L2,
-    // which costs the other workgroups their cached x and codes.
-    constexpr int kPer = FM * FN * 16;
-    // Partials through a buffer descriptor with the sc1 cache policy
+  if (splits == 1) {
+    store_direct<T, BM, BN, WM, WN, MC>(g, acc, m0, n0, 0, lane, wm, wn);
+  } else {
+    // K range z of the tile: contributors z = 0 .. splits - 1 (K order),
+    // partial slot tile splits + z.
+    const int nc = splits, me = z;
+    auto slot = [&](int idx) { return tile * splits + idx; };
+    // Partial tiles through a buffer descriptor with the sc1 cache policy
     // (device-coherent: write-through stores, loads that miss stale
-    // lines), 16 bytes per lane: four values r = 4 u .. 4 u + 3 of
-    // fragment q = i FN + j of thread t at float4 (q 4 + u) NT + t.
-    const long long wsbytes = static_cast<long long>(ntiles) * splits * kPer *
-                              C::NT * 4;
+    // lines), 16 bytes per lane: values 4 u .. 4 u + 3 of fragment
+    // q = i FN + j of thread t at float4 ((slot kPer / 4) + q 4 + u) NT + t
+    // (coalesced). The order "partial, then arrival" comes from waiting
+    // for the stores to complete before the device-scope counter is
+    // incremented; a device-scope fence would do the same by writing back
+    // and invalidating the whole L2, which costs the other workgroups
+    // their cached x and codes.
+    constexpr int kPer = FM * FN * 16;
     const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(
-        g.ws, (short)0,
-        static_cast<int>(wsbytes < 0x7FFFFFFFll ? wsbytes : 0x7FFFFFFFll),
-        0x00020000);
+        g.ws, (short)0, 0x7FFFFFFF, 0x00020000);
     constexpr int kSc1 = 16;
-    auto part_off = [&](int zz, int q, int u) {
-      return ((((tile * splits + zz) * kPer / 4) + q * 4 + u) * C::NT + tid) *
-             16;
+    auto part_off = [&](int sl, int q, int u) {
+      return (((sl * (kPer / 4)) + q * 4 + u) * C::NT + tid) * 16;
     };
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -435,7 +435,7 @@ qgemm_dma_kernel(GemmArgs g) {
           f32x4 v = {acc[i][j][4 * u], acc[i][j][4 * u + 1],
                      acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]};
           __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(u32x4, v), wsr, part_off(z, i * FN + j, u),
+              __builtin_bit_cast(u32x4, v), wsr, part_off(slot(me), i * FN + j, u),
               0, kSc1);
         }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -444,61 +444,62 @@ qgemm_dma_kernel(GemmArgs g) {
     if (tid == 0) {
       const uint32_t old = __hip_atomic_fetch_add(
           g.wsflag + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const uint32_t last = old + 1 == static_cast<uint32_t>(splits);
+      const uint32_t last = old + 1 == static_cast<uint32_t>(nc);
       if (last)
         __hip_atomic_store(g.wsflag + tile, 0u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
       *flag = last;
     }
     __syncthreads();
-    if (*flag == 0) return;
-    // The sum in the order z = 0, 1, ... (the result does not depend on
-    // which workgroup arrived last), four fragments at a time: the 64
-    // loads of one partial's share are all issued before they are added,
-    // so each partial costs one memory round trip.
-    constexpr int kFrags = FM * FN;
-    constexpr int kChunk = kFrags < 4 ? kFrags : 4;
+    if (*flag != 0) {
+      // The sum in K order, ((p0 + p1) + p2) + ..., in place: the own
+      // partial stands first when me <= 1 (the first addition commutes);
+      // for me >= 2 the sum restarts from p0 and reloads the own partial
+      // in its place. kChunk fragments at a time, all loads of a chunk
+      // issued together (one memory round trip per partial and chunk).
+      constexpr int kFrags = FM * FN;
+      constexpr int kChunk =
+          C::NT <= 256 ? kFrags : (kFrags < 4 ? kFrags : 4);
+      const int start = me >= 2 ? 1 : 0;
 #pragma unroll
-    for (int q0 = 0; q0 < kFrags; q0 += kChunk) {
-      float t[kChunk][16];
-#pragma unroll
-      for (int q = 0; q < kChunk; ++q)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) t[q][r] = 0.f;
-      for (int zz = 0; zz < splits; ++zz) {
-        float v[kChunk][16];
-        if (zz == z) {
-#pragma unroll
-          for (int q = 0; q < kChunk; ++q)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-              v[q][r] = acc[(q0 + q) / FN][(q0 + q) % FN][r];
-        } else {
+      for (int q0 = 0; q0 < kFrags; q0 += kChunk) {
+        auto load_into = [&](int idx, float (&v)[kChunk][16]) {
+          const int sl = slot(idx);
 #pragma unroll
           for (int q = 0; q < kChunk; ++q)
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
               const f32x4 l = __builtin_bit_cast(
                   f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                             wsr, part_off(zz, q0 + q, u), 0, kSc1));
+                             wsr, part_off(sl, q0 + q, u), 0, kSc1));
 #pragma unroll
               for (int e = 0; e < 4; ++e) v[q][4 * u + e] = l[e];
             }
+        };
+        float v[kChunk][16];
+        if (me >= 2) {
+          load_into(0, v);
+#pragma unroll
+          for (int q = 0; q < kChunk; ++q)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              acc[(q0 + q) / FN][(q0 + q) % FN][r] = v[q][r];
         }
+        for (int idx = start; idx < nc; ++idx) {
+          if (idx == me && me <= 1) continue;
+          load_into(idx, v);
 #pragma unroll
-        for (int q = 0; q < kChunk; ++q)
+          for (int q = 0; q < kChunk; ++q)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) t[q][r] += v[q][r];
+            for (int r = 0; r < 16; ++r)
+              acc[(q0 + q) / FN][(q0 + q) % FN][r] += v[q][r];
+        }
       }
-#pragma unroll
-      for (int q = 0; q < kChunk; ++q)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          acc[(q0 + q) / FN][(q0 + q) % FN][r] = t[q][r];
+      store_direct<T, BM, BN, WM, WN, MC>(g, acc, m0, n0, 0, lane, wm, wn);
     }
   }
-  store_direct<T, BM, BN, WM, WN, MC>(g, acc, m0, n0, 0, lane, wm, wn);
 }
+
 
 }  // namespace
 }  // namespace qk
