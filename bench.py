@@ -261,17 +261,27 @@ def secondary(torch, qkern, dev, gen):
         # rownorm [4096, 4096]
         # (LayerNorm with gain and offset, eps 1e-5, beside the configured
         # RMSNorm and softmax)
-        for name, kind, dt, esz in [("rmsnorm bf16", 0, torch.bfloat16, 2),
-                                    ("rmsnorm f32", 0, torch.float32, 4),
-                                    ("softmax f32", 2, torch.float32, 4),
-                                    ("layernorm bf16", 1, torch.bfloat16, 2)]:
+        # params: "f32" gain/offset in f32, "none" without them (the
+        # reference's layernorm, bench/jax_bench.py:44-46), "same" in x's
+        # type
+        for name, kind, dt, esz, params in [
+                ("rmsnorm bf16", 0, torch.bfloat16, 2, "f32"),
+                ("rmsnorm f32", 0, torch.float32, 4, "f32"),
+                ("softmax f32", 2, torch.float32, 4, "f32"),
+                ("layernorm bf16", 1, torch.bfloat16, 2, "none"),
+                ("layernorm bf16 + bf16 gain/offset", 1, torch.bfloat16, 2,
+                 "same"),
+                ("layernorm bf16 + f32 gain/offset", 1, torch.bfloat16, 2,
+                 "f32")]:
             xs = [torch.randn(4096, 4096, device=dev, generator=gen).to(dt)
                   for _ in range(8)]
             ys = [torch.empty_like(xs[0]) for _ in range(2)]
             g = (1 + 0.1 * torch.randn(4096, device=dev, generator=gen))
             bt = 0.1 * torch.randn(4096, device=dev, generator=gen)
-            gain = g if kind != 2 else None
-            beta = bt if kind == 1 else None
+            if params == "same":
+                g, bt = g.to(dt), bt.to(dt)
+            gain = g if kind != 2 and params != "none" else None
+            beta = bt if kind == 1 and params != "none" else None
             eps = 1e-5 if kind == 1 else 1e-6
             fn = lambda i: qkern.rownorm(xs[i % 8], kind, eps=eps, gain=gain,
                                          beta=beta, out=ys[i % 2])

@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 
 #include "qk_device.h"
 #include "qk_internal.h"
@@ -262,7 +263,11 @@ __global__ __launch_bounds__(kThreads) void rownorm_kernel(RnArgs a) {
 // workgroup step through their rows together, so the loop's trip count and
 // its barriers are uniform across the workgroup (rows past the end go
 // through the zero-extent descriptors like any other).
-template <typename T, int KIND, int V, int VPT, int SPLIT = 1>
+//
+// PL: gain and offset in T's type (16-byte aligned) or absent, kept
+// packed in registers (LayerNorm of 16-bit rows of 8 vectors per
+// lane: one wave per row at two waves per SIMD, no barriers per row).
+template <typename T, int KIND, int V, int VPT, int SPLIT = 1, bool PL = false>
 __global__ __launch_bounds__(kThreads) void rownorm_stream_kernel(RnArgs a) {
   static_assert(V > 1, "vector rows only");
   static_assert(SPLIT == 1 || SPLIT == 2, "one or two waves per row");
@@ -296,8 +301,28 @@ __global__ __launch_bounds__(kThreads) void rownorm_stream_kernel(RnArgs a) {
 
   constexpr bool kParams = KIND != QK_ROWNORM_SOFTMAX;
   constexpr bool kBeta = KIND == QK_ROWNORM_LAYER;
-  float g[kParams ? VPT : 1][V], bb[kBeta ? VPT : 1][V];
-  if constexpr (kParams) {
+  static_assert(!PL || (SPLIT == 1 && V == 8), "packed parameters");
+  // PL: gain and offset of T's type kept packed (16-byte vectors of V
+  // values) and widened when used.
+  u32x4 gpk[PL ? VPT : 1], bpk[PL ? VPT : 1];
+  if constexpr (PL) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int base = (lane + i * 64) * V;
+      const bool in = base < n;
+      // absent: gain 1.0, offset 0 (as pairs of T)
+      const uint32_t one2 = std::is_same<T, bf16>::value ? 0x3F803F80u
+                                                         : 0x3C003C00u;
+      gpk[i] = in && a.has_gain ? *reinterpret_cast<const u32x4*>(
+                                      static_cast<const T*>(a.gain) + base)
+                                : u32x4{one2, one2, one2, one2};
+      bpk[i] = in && a.has_beta ? *reinterpret_cast<const u32x4*>(
+                                      static_cast<const T*>(a.beta) + base)
+                                : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  float g[kParams && !PL ? VPT : 1][V], bb[kBeta && !PL ? VPT : 1][V];
+  if constexpr (kParams && !PL) {
     const bool gvec = (reinterpret_cast<uintptr_t>(a.gain) % 16 == 0);
     const bool bvec = (reinterpret_cast<uintptr_t>(a.beta) % 16 == 0);
 #pragma unroll
@@ -356,6 +381,31 @@ __global__ __launch_bounds__(kThreads) void rownorm_stream_kernel(RnArgs a) {
       scale = rsqrtf(combine(wave_sum_dpp(ss), par, 0, false) /
                          static_cast<float>(n) +
                      a.eps);
+    } else if constexpr (KIND == QK_ROWNORM_LAYER && PL) {
+      // 16-bit rows: mean and variance from one reduction of the sums of
+      // d = x - x0 and d^2, shifted by the row's first element x0 (a
+      // sample of the row, so the two sums do not cancel; 16-bit inputs
+      // leave the f32 sums far inside the output's rounding).
+      const float x0 = __builtin_bit_cast(
+          float, __builtin_amdgcn_readfirstlane(
+                     __builtin_bit_cast(int, v[0][0])));
+      float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const bool in = (vbase + lane + i * 64) * V < n;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const float d = in ? v[i][e] - x0 : 0.f;
+          s1 += d;
+          s2 = fmaf(d, d, s2);
+        }
+      }
+      // two independent DPP reductions (their steps interleave)
+      const float inv_n = 1.f / static_cast<float>(n);
+      const float m1 = wave_sum_dpp(s1) * inv_n;
+      const float m2 = wave_sum_dpp(s2) * inv_n;
+      shift = x0 + m1;
+      scale = 1.0f / sqrtf(fmaxf(m2 - m1 * m1, 0.f) + a.eps);
     } else if constexpr (KIND == QK_ROWNORM_LAYER) {
       float s = 0.f;
 #pragma unroll
@@ -399,11 +449,26 @@ __global__ __launch_bounds__(kThreads) void rownorm_stream_kernel(RnArgs a) {
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       Pack q;
+      float gp[V], bp[V];
+      if constexpr (PL) {
+        Pack gq, bq;
+        gq.u = gpk[i];
+        bq.u = bpk[i];
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          gp[e] = to_f32(gq.e[e]);
+          bp[e] = to_f32(bq.e[e]);
+        }
+      }
 #pragma unroll
       for (int e = 0; e < V; ++e) {
         float o = (v[i][e] - shift) * scale;
-        if constexpr (kParams) o *= g[i][e];
-        if constexpr (kBeta) o += bb[kBeta ? i : 0][e];
+        if constexpr (PL) {
+          o = o * gp[e] + bp[e];
+        } else {
+          if constexpr (kParams) o *= g[i][e];
+          if constexpr (kBeta) o += bb[kBeta ? i : 0][e];
+        }
         q.e[e] = from_f32<T>(o);
       }
       // Offsets at or past the row end are dropped by the descriptor.
@@ -524,8 +589,22 @@ bool LaunchStream(const RnArgs& a, hipStream_t st) {
   // LayerNorm of 16-bit rows (gain and offset held as f32): 8 vectors per
   // lane take 256 VGPRs, one wave per SIMD; two waves of 4 keep two per
   // SIMD ([4096, 4096] bf16: 16.7 -> 14.5 us).
-  if (KIND == QK_ROWNORM_LAYER && V == 8 && a.n <= 64 * V * 8)
-    return go(rownorm_stream_kernel<T, KIND, V, 4, 2>, 2);
+  if constexpr (KIND == QK_ROWNORM_LAYER && V == 8) {
+    // Gain and offset each absent (the reference's layernorm has neither)
+    // or of x's type and 16-byte aligned: held packed, one wave per row;
+    // else two waves of 4 vectors per row with the parameters in f32.
+    const int tcode = std::is_same<T, bf16>::value ? QK_BF16 : QK_F16;
+    auto packable = [&](bool has, const void* q, int dt) {
+      return !has || (dt == tcode && reinterpret_cast<uintptr_t>(q) % 16 == 0);
+    };
+    const bool packed_params = packable(a.has_gain, a.gain, a.gdt) &&
+                               packable(a.has_beta, a.beta, a.bdt) &&
+                               std::getenv("QK_ROWNORM_LAYER_SPLIT") == nullptr;
+    if (a.n <= 64 * V * 8)
+      return packed_params
+                 ? go(rownorm_stream_kernel<T, KIND, V, 8, 1, true>)
+                 : go(rownorm_stream_kernel<T, KIND, V, 4, 2>, 2);
+  }
   if (a.n <= 64 * V * 8) return go(rownorm_stream_kernel<T, KIND, V, 8>);
   if (a.n <= 64 * V * 16)
     return go(rownorm_stream_kernel<T, KIND, V, 8, 2>, 2);

@@ -112,6 +112,22 @@ def test_rownorm_many_rows(dev, kind, dtype):
             pdtype)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_layer_norm_packed_parameters(dev, dtype):
+    """16-bit layer norm rows of up to 8 vectors per lane whose gain and
+    offset are absent (the reference's layernorm, bench/jax_bench.py:44-46)
+    or of the row's type, singly or together: one wave per row with the
+    parameters held packed (a partly filled last vector per lane at
+    n = 3000)."""
+    rng = np.random.default_rng(77)
+    for n in (4096, 3000):
+        x = rng.standard_normal((4100, n)) + 0.3
+        gain = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        beta = (0.1 * rng.standard_normal(n)).astype(np.float32)
+        for g, b in ((None, None), (gain, None), (None, beta), (gain, beta)):
+            run(dev, RownormKind.LAYER, x, dtype, g, b, 1e-5, dtype)
+
+
 def test_rownorm_no_gain_and_leading_dims(dev):
     rng = np.random.default_rng(3)
     x = rng.standard_normal((2, 3, 5, 96))
