@@ -164,6 +164,26 @@ struct QTileCodes {
   }
 };
 
+// f(kt + I, integral_constant<I>) for I = 0 .. N - 1 (the stage index a
+// compile-time constant), and the same stopping at the first kt + I past
+// kend.
+template <int I, int N, typename F>
+__device__ __forceinline__ void QTiles(F& f, int kt) {
+  if constexpr (I < N) {
+    f(kt + I, std::integral_constant<int, I>{});
+    QTiles<I + 1, N>(f, kt);
+  }
+}
+template <int I, int N, typename F>
+__device__ __forceinline__ void QTilesTail(F& f, int kt, int kend) {
+  if constexpr (I < N) {
+    if (kt + I < kend) {
+      f(kt + I, std::integral_constant<int, I>{});
+      QTilesTail<I + 1, N>(f, kt, kend);
+    }
+  }
+}
+
 // MC: M need not be a multiple of BM (A rows past M read zeros through
 // the descriptor's extent; their outputs are not stored). K is a multiple
 // of 512 (whole scale blocks), and so is every split's K range.
@@ -384,23 +404,10 @@ qgemm_dma_kernel(GemmArgs g) {
     for (int j = 0; j < FN; ++j)
       fb[0][j] = cw[j].template dq<T>(0, scl[j], bil[j]);
   };
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
-  static_assert(S == 3 || S == 4, "unrolled for three or four stages");
+  static_assert(S >= 3, "at least three stages");
   int kt = kbeg;
-  for (; kt + S <= kend; kt += S) {
-    tile_step(kt, I0{});
-    tile_step(kt + 1, I1{});
-    tile_step(kt + 2, I2{});
-    if constexpr (S == 4) tile_step(kt + 3, I3{});
-  }
-  if (kt < kend) tile_step(kt, I0{});
-  if (kt + 1 < kend) tile_step(kt + 1, I1{});
-  if constexpr (S == 4) {
-    if (kt + 2 < kend) tile_step(kt + 2, I2{});
-  }
+  for (; kt + S <= kend; kt += S) QTiles<0, S>(tile_step, kt);
+  QTilesTail<0, S - 1>(tile_step, kt, kend);
   // No DMA may still be writing this workgroup's LDS when it ends.
   __builtin_amdgcn_s_waitcnt(VmcntImm(0));
   if (splits == 1) {

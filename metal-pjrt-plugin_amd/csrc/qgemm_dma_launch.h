@@ -21,16 +21,20 @@ constexpr QDmaCfg kQDmaCfgs[] = {
     {256, 128, 1, 1}, {128, 256, 1, 1}, {128, 128, 2, 1}};
 constexpr int kQDmaNumCfgs = sizeof(kQDmaCfgs) / sizeof(kQDmaCfgs[0]);
 
-// A stages: four when they fit the LDS with the code and scale blocks,
-// else three; 0 when not even three fit (the layout of QDma).
+// A stages: the most (up to kQDmaMaxStages) that fit the LDS with the
+// code and scale blocks; 0 when not even three fit (the layout of QDma).
+constexpr int kQDmaMaxStages = 4;
 template <int PACK, int BM, int BN, int WM, int FN>
 constexpr int QDmaStages() {
   constexpr int crow = (PACK == QK_PACK_U32X8 ? 32 : 64) * 2;
   constexpr int nw = WM * BN / (32 * FN);
   constexpr int pad = (BM / 8) % nw != 0 ? 1024 : 0;
-  constexpr int b4 = 4 * BM * 128 + 3 * BN * crow + 4 * BN * 16 + pad;
-  constexpr int b3 = 3 * BM * 128 + 2 * BN * crow + 4 * BN * 16 + pad;
-  return b4 <= 160 * 1024 ? 4 : b3 <= 160 * 1024 ? 3 : 0;
+  int best = 0;
+  for (int s = 3; s <= kQDmaMaxStages; ++s)
+    if (s * BM * 128 + (s / 2 + 1) * BN * crow + 4 * BN * 16 + pad <=
+        160 * 1024)
+      best = s;
+  return best;
 }
 
 template <int PACK, int I>
