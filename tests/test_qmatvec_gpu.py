@@ -284,6 +284,70 @@ def test_qgemm_dma_tiles_and_k_splits(dev, packing, monkeypatch):
                      O.round_to(w, "float16"))
 
 
+@pytest.mark.parametrize("packing", [Packing.U32X8, Packing.U8])
+def test_qgemm_dma_routing_edges(dev, packing):
+    """Row counts at the routing boundary (64: the K-split kernel of the
+    workgroup's waves where it applies, 65: the register-dequantizing
+    GEMM), one 512-wide K block (no K split possible), a single 128-column
+    tile, and many rows (256 x 128 tiles), against the float64 oracle."""
+    for m, n, k in ((64, 384, 1024), (65, 384, 1024), (70, 128, 512),
+                    (300, 256, 512), (130, 4096, 512)):
+        rng = np.random.default_rng(m + n + k)
+        dc, ds, db, w, *_ = make_weights(rng, n, k, packing, 64)
+        x = O.round_to(rng.standard_normal((m, k)), "bfloat16").astype(
+            np.float32)
+        y = qkern.qmatvec(torch.from_numpy(x).to(torch.bfloat16).to(dev),
+                          dc.to(dev), ds.to(dev), db.to(dev), packing=packing)
+        torch.cuda.synchronize()
+        check_matvec(y.float().cpu().numpy().astype(np.float64), x,
+                     O.round_to(w, "bfloat16"))
+
+
+def test_qgemm_dma_split_workspace_growth_and_graph(dev, monkeypatch):
+    """The K split's library workspace: a small split problem, then one
+    needing a larger workspace (a new allocation), then the small one again
+    on the same stream; then the larger problem captured into a HIP graph
+    on a fresh stream (whose workspace is made first by an eager call on
+    it) and replayed three times with eager work between the replays,
+    every replay checked against the eager result bit for bit."""
+    rng = np.random.default_rng(5)
+    cases = []
+    for n in (512, 4096):
+        dc, ds, db, w, *_ = make_weights(rng, n, 4096, Packing.U32X8, 64)
+        x = O.round_to(rng.standard_normal((128, 4096)),
+                       "bfloat16").astype(np.float32)
+        cases.append((torch.from_numpy(x).to(torch.bfloat16).to(dev),
+                      (dc.to(dev), ds.to(dev), db.to(dev)), x,
+                      O.round_to(w, "bfloat16")))
+    monkeypatch.setenv("QK_QGEMM_DMA", "2,8")  # 128 x 128 tiles, K split 8
+    for i in (0, 1, 0):
+        xd, args, x, want_w = cases[i]
+        y = qkern.qmatvec(xd, *args)
+        torch.cuda.synchronize()
+        check_matvec(y.float().cpu().numpy().astype(np.float64), x, want_w)
+    xd, args, x, want_w = cases[1]
+    eager = qkern.qmatvec(xd, *args)
+    torch.cuda.synchronize()
+    out = torch.empty_like(eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        qkern.qmatvec(xd, *args, out=out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            qkern.qmatvec(xd, *args, out=out)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.fill_(7.0)
+        qkern.qmatvec(cases[0][0], *cases[0][1])  # eager work between
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
 def test_qmatvec_leading_dims_and_no_bias(dev):
     rng = np.random.default_rng(5)
     dc, ds, _, w, *_ = make_weights(rng, 40, 256, Packing.U32X8, 64,
