@@ -163,7 +163,10 @@ bool StreamWorkspace(hipStream_t stream, size_t bytes, float** ws,
     (void)hipGetLastError();
     return false;
   }
-  const size_t size = std::max<size_t>(need, size_t{32} << 20);
+  // At least double the previous size: the replaced buffers (kept alive)
+  // then total less than the largest one.
+  const size_t size = std::max<size_t>(
+      std::max<size_t>(need, size_t{32} << 20), e != nullptr ? 2 * e->bytes : 0);
   // A smaller buffer being replaced is not freed: launches still queued
   // on the stream, and graphs captured from it, keep using it.
   void* p = nullptr;

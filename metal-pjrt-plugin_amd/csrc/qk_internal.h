@@ -45,9 +45,11 @@ int DeviceComputeUnits();
 
 // Split-K workspace owned by the library, one per (device, stream): *ws
 // takes at least `bytes` of f32 partials, *flags kWsFlagBytes / 4 arrival
-// counters (zero between launches). Grown on demand by a new allocation
-// (the old one stays valid for launches already queued and for graphs
-// captured from the stream), never freed before the process ends.
+// counters (zero between launches). Grown on demand by a new allocation of
+// at least twice the size (the old one stays valid for launches already
+// queued and for graphs captured from the stream, so all of a stream's
+// buffers together stay under twice its largest), never freed before the
+// process ends.
 // Launches on one stream run in order, so they never use it concurrently;
 // a captured graph keeps its capture stream's buffer, so its replays must
 // not overlap other launches on that stream. False while the stream is
