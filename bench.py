@@ -378,6 +378,31 @@ def secondary_more(torch, qkern, dev, gen):
                     "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
                     "frac": round(gbs / HBM_PEAK_GBS, 4)})
         del words, s, b, rows
+    if want("quantize"):
+        # Checkpoint quantization on the device (qk_quantize): a Qwen3-8B
+        # projection 12288 x 4096 bf16 to int4 u32x8 codes with f32 scales
+        # and offsets; bytes = weights read + codes, scales, offsets written
+        n, k = 12288, 4096
+        ws = [(0.02 * torch.randn(n, k, device=dev, generator=gen)).to(
+            torch.bfloat16) for _ in range(4)]
+        codes = torch.empty(n, k // 8, dtype=torch.int32, device=dev)
+        sc = torch.empty(n, k // GROUP, dtype=torch.float32, device=dev)
+        of = torch.empty_like(sc)
+        from qkern.ffi import _attrs, any_buffer, check, lib, _ref
+        import ctypes
+        bufs = [tuple(any_buffer(t) for t in (w, codes, sc, of)) for w in ws]
+        at = _attrs(qkern.Packing.U32X8, GROUP, True)
+        fn = lambda i: check(lib().qk_quantize(
+            qkern.blas.stream_handle(None), *(_ref(b) for b in bufs[i % 4]),
+            ctypes.byref(at)))
+        fn(0)
+        ms = timed_launches(torch, fn, 16)
+        nbytes = n * k * 2 + n * k // 2 + 2 * n * (k // GROUP) * 4
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"name": "int4 quantize 12288x4096 bf16 (qk_quantize)",
+                    "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del ws, codes, sc, of
     if want("copy"):
         # The practical read+write ceiling: a plain device copy of the rownorm
         # sizes (rotating over 8 sources, 537 MB or more)
@@ -443,6 +468,17 @@ def cpu_secondary(seconds=3.0):
     dt = rate(lambda: torch.softmax(x, -1))
     res.append({"name": "softmax f32 4096x4096",
                 "value": round(2 * 4096 * 4096 * 4 / dt / 1e9, 2),
+                "unit": "GB/s"})
+    # the host quantizer (the reference's loader quantizes in numpy,
+    # examples/llm/qwen3.py:169-196): qkern.quant on a 2048 x 4096 slice
+    from qkern import quant
+    wq = (0.02 * torch.randn(2048, 4096, generator=g)).to(
+        torch.bfloat16).float().numpy()
+    dt = rate(lambda: quant.pack_u32x8(quant.quantize_int4(wq)[0]))
+    res.append({"name": "int4 quantize 12288x4096 bf16 (numpy, 2048-row "
+                        "slice)",
+                "value": round(2048 * (4096 * 2 + 4096 // 2 + 64 * 8) / dt /
+                               1e9, 2),
                 "unit": "GB/s"})
     return {"impl": "torch CPU (float32 arithmetic, bf16 rounding of the "
                     "output), in place of JAX_PLATFORMS=cpu: jax is not "

@@ -234,6 +234,20 @@ qk_status qk_dequantize(void* stream, const qk_buffer* codes,
                         const qk_buffer* scales, const qk_buffer* biases,
                         qk_buffer* w, const qk_quant_attrs* attrs);
 
+/* Quantizes w [N, K] (f32, f16 or bf16, 16-byte aligned) into the codes,
+ * scales and offsets qk$qmatvec reads (all outputs, shaped as qk_qmatvec
+ * takes them for attrs): int4 affine (U32X8 or BYTE_HALFSPLIT; biases
+ * required, has_bias = 1) on the MLX-style grid of quantize_int4
+ * (examples/llm/qwen3.py:169-196), or symmetric int8 (S8_SYM; no biases)
+ * as quantize_int8 (qwen3.py:154-166). Bit-identical to those float32
+ * computations; scales and offsets (one dtype) are stored in f32 or
+ * rounded once to f16 / bf16. U8 (affine 8-bit) has no reference
+ * quantizer: QK_UNIMPLEMENTED. Replaces the host quantization the
+ * reference's load_params does per matrix (qwen3.py:113-128). */
+qk_status qk_quantize(void* stream, const qk_buffer* w, qk_buffer* codes,
+                      qk_buffer* scales, qk_buffer* biases,
+                      const qk_quant_attrs* attrs);
+
 typedef enum {
   QK_ROWNORM_RMS = 0,     /* y = x * rsqrt(mean(x^2) + eps) * gain */
   QK_ROWNORM_LAYER = 1,   /* y = (x - mean) / sqrt(var + eps) * gain + beta */

@@ -845,6 +845,55 @@ extern "C" qk_status qk_dequantize(void* stream, const qk_buffer* codes,
   return qk::LaunchDequantize(q, static_cast<hipStream_t>(stream));
 }
 
+extern "C" qk_status qk_quantize(void* stream, const qk_buffer* w,
+                                 qk_buffer* codes, qk_buffer* scales,
+                                 qk_buffer* biases,
+                                 const qk_quant_attrs* attrs) {
+  if (qk_status s = CheckBuffer(w, "w", false); s != QK_OK) return s;
+  if (!IsFloat(w->dtype) || w->rank != 2) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: quantize input must be float [N, K], got " +
+                    BufferString(*w));
+  }
+  qk::QuantProblem q;
+  if (qk_status s = CheckQuant(codes, scales, biases, attrs, w->dims[1], &q);
+      s != QK_OK) {
+    return s;
+  }
+  if (attrs->packing == QK_PACK_U8) {
+    return Fail(QK_UNIMPLEMENTED,
+                "qkern: quantize makes int4 affine (u32x8, byte_halfsplit) or "
+                "symmetric int8 (s8_sym) codes, as the reference's quantizers "
+                "do; there is no 8-bit affine quantizer");
+  }
+  const bool int4 = attrs->bits == 4;
+  if (int4 && (!attrs->has_bias || biases == nullptr)) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: int4 quantization writes offsets: pass biases and "
+                "has_bias = 1");
+  }
+  if (w->dims[0] != q.n) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: quantize input has " + std::to_string(w->dims[0]) +
+                    " rows, codes have " + std::to_string(q.n));
+  }
+  if (int4 && biases->dtype != scales->dtype) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: quantize writes scales and offsets of one dtype, got " +
+                    BufferString(*scales) + " and " + BufferString(*biases));
+  }
+  if (reinterpret_cast<uintptr_t>(w->data) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(codes->data) % 4 != 0) {
+    return Fail(QK_INVALID_ARGUMENT,
+                "qkern: quantize needs 16-byte aligned weights and 4-byte "
+                "aligned codes");
+  }
+  if (q.n == 0 || q.k == 0) return QK_OK;
+  if (qk_status s = qk::PreLaunch(); s != QK_OK) return s;
+  return qk::LaunchQuantize(q, w->data, w->dtype,
+                            static_cast<hipStream_t>(stream));
+}
+
 extern "C" qk_status qk_embed(void* stream, const qk_buffer* tokens,
                               const qk_buffer* table, const qk_buffer* scales,
                               const qk_buffer* biases, qk_buffer* out,

@@ -149,6 +149,10 @@ bool QGemmDmaApplies(const QuantProblem& p);
 qk_status LaunchQGemmDma(const QuantProblem& p, hipStream_t stream);
 qk_status LaunchQGemm(const QuantProblem& p, hipStream_t stream);
 qk_status LaunchDequantize(const QuantProblem& p, hipStream_t stream);
+// The quantizer (quantize.hip): w [n, k] of w_dtype into p's codes, scales
+// and offsets (outputs; scale and offset dtype p.scale_dtype).
+qk_status LaunchQuantize(const QuantProblem& p, const void* w, int w_dtype,
+                         hipStream_t stream);
 
 // Dense embedding gather: out[t, :] = table[clamp(rows[t]), :] (k elements
 // of esz bytes per row; table rows ld elements apart).

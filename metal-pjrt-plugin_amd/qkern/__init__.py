@@ -5,7 +5,9 @@ Three kernel families behind a C ABI (include/qkern.h, libqkern.so):
   - ffi:   qk$qmatvec / qk$dequantize (int4 / int8 group-affine weights)
            qk$rownorm (RMSNorm, LayerNorm, softmax) and
            qk$decode_attention (one query against the KV cache);
-  - quant: host-side quantizers and packers for the weight formats.
+  - quant: host-side quantizers and packers for the weight formats;
+  - weights: safetensors reading and quantization on the device
+           (qk_quantize).
 Every compute call runs a HIP kernel; there is no CPU fallback.
 """
 
@@ -16,7 +18,8 @@ from .ffi import (Packing, RownormKind, decode_attention,  # noqa: F401
                   decode_attention_noalloc,
                   decode_attention_workspace_size, dequantize, embed,
                   layer_norm,
-                  qmatvec, rms_norm, rownorm, softmax)
+                  qmatvec, quantize, rms_norm, rownorm, softmax)
+from .weights import load_quantized, read_safetensors  # noqa: F401
 
 
 def version():

@@ -83,6 +83,9 @@ SIGNATURES = {
     "qk_dequantize": (ctypes.c_int, [ctypes.c_void_p, _P(BufferC), _P(BufferC),
                                      _P(BufferC), _P(BufferC),
                                      _P(QuantAttrsC)]),
+    "qk_quantize": (ctypes.c_int, [ctypes.c_void_p, _P(BufferC), _P(BufferC),
+                                   _P(BufferC), _P(BufferC),
+                                   _P(QuantAttrsC)]),
     "qk_rownorm": (ctypes.c_int, [ctypes.c_void_p, _P(BufferC), _P(BufferC),
                                   _P(BufferC), _P(BufferC),
                                   _P(RownormAttrsC)]),

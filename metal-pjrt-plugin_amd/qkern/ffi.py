@@ -99,6 +99,35 @@ def dequantize(codes, scales, biases=None, *, k, packing=Packing.U32X8,
     return out
 
 
+def quantize(w, *, packing=Packing.U32X8, group_size=64,
+             scale_dtype=torch.float32, stream=None):
+    """qk_quantize: the codes, scales and offsets of w [N, K] (f32 / f16 /
+    bf16 on the device) on the reference's grids (examples/llm/qwen3.py:
+    154-196): int4 affine for U32X8 / BYTE_HALFSPLIT, symmetric int8 for
+    S8_SYM. Returns (codes, scales, offsets or None) laid out as qmatvec
+    takes them: U32X8 int32 [N, K/8], BYTE_HALFSPLIT uint8 [N, K/g, g/2],
+    S8_SYM int8 [N, K]; scales / offsets [N, K/g] in scale_dtype."""
+    packing = Packing(packing)
+    n, k = w.shape
+    g = group_size
+    dev = w.device
+    if packing == Packing.U32X8:
+        codes = torch.empty(n, k // 8, dtype=torch.int32, device=dev)
+    elif packing == Packing.BYTE_HALFSPLIT:
+        codes = torch.empty(n, k // g, g // 2, dtype=torch.uint8, device=dev)
+    else:
+        codes = torch.empty(n, k, dtype=torch.int8 if packing ==
+                            Packing.S8_SYM else torch.uint8, device=dev)
+    scales = torch.empty(n, k // g, dtype=scale_dtype, device=dev)
+    int4 = packing in (Packing.U32X8, Packing.BYTE_HALFSPLIT)
+    biases = torch.empty_like(scales) if int4 else None
+    bw, bc, bs, bb = (any_buffer(t) for t in (w, codes, scales, biases))
+    attrs = _attrs(packing, group_size, int4)
+    check(lib().qk_quantize(stream_handle(stream), _ref(bw), _ref(bc),
+                            _ref(bs), _ref(bb), ctypes.byref(attrs)))
+    return codes, scales, biases
+
+
 def embed(table, tokens, scales=None, biases=None, *, k=None,
           packing=Packing.U32X8, group_size=64, dtype=None, out=None,
           stream=None):
