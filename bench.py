@@ -9,9 +9,12 @@ copies of the weight set (1.25 GB) are rotated so that no launch reads
 weights another launch left in the 256 MB Infinity Cache.
 
 Also reported (`secondary`): bf16 GEMM + bias + SiLU TFLOP/s at the C3
-shapes (the metric's second half), int4 M = 16 / 512, int8 affine GEMV,
-RMSNorm, softmax and LayerNorm [4096, 4096] HBM GB/s; each against its
-roofline.
+shapes (the metric's second half, beside hipBLASLt), f32 GEMM 1024^3,
+int4 M = 16 / 512 at the four Qwen3-8B shapes, int8 affine M = 1 / 8 / 128,
+RMSNorm, softmax and LayerNorm [4096, 4096], the reference's few-row GEMM
+list, decode attention, the int4 embedding gather, device quantization of
+a projection and device copies (the read + write ceiling); each against
+its roofline. `--only PART,...` runs chosen secondary parts alone.
 
 Timing: the W warm-up steps and the K timed steps are each captured into a
 HIP graph (the launches only: outputs are preallocated, nothing is

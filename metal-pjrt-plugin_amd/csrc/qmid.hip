@@ -1,4 +1,5 @@
-// Quantized matmul for a medium number of rows of x (33..128 as routed):
+// Quantized matmul for a medium number of rows of x (33..64 as routed,
+// and up to 128 where the register-dequantizing GEMM does not apply):
 // y[M, N] = x[M, K] W^T, W int8 (u8 affine or s8 symmetric) or int4 (u32x8
 // words), bf16 x / scale / offset, group size 64 — the short-prefill
 // shapes. The reference's linear() (examples/llm/qwen3.py:215-230)
