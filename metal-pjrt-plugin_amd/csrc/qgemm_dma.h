@@ -465,8 +465,9 @@ qgemm_dma_kernel(GemmArgs g) {
       // in its place. kChunk fragments at a time, all loads of a chunk
       // issued together (one memory round trip per partial and chunk).
       constexpr int kFrags = FM * FN;
-      constexpr int kChunk =
-          C::NT <= 256 ? kFrags : (kFrags < 4 ? kFrags : 4);
+      // (Two fragments, 32 values: a larger chunk raised the register
+      // count of the whole kernel into spills.)
+      constexpr int kChunk = kFrags < 2 ? kFrags : 2;
       const int start = me >= 2 ? 1 : 0;
 #pragma unroll
       for (int q0 = 0; q0 < kFrags; q0 += kChunk) {
