@@ -18,10 +18,11 @@
 // (nearest even) to f16 / bf16.
 //
 // One thread per group (its 32..128 weights in registers, read as 16-byte
-// vectors). The correctly rounded divisions (one per weight) are the larger
-// cost: 12288 x 4096 bf16 in 32 us (4.1 TB/s of weights read and codes
-// written); eight lanes per group with the extremes reduced across them
-// measured slower (3.4 TB/s: the per-group divisions repeat on every lane).
+// vectors); each weight's quotient rounded through the reciprocal, with
+// the correctly rounded division only near a rounding boundary (one per
+// weight made the kernel division-bound: 32 against 28.6 us at 12288 x 4096
+// bf16). Eight lanes per group with the extremes reduced across them
+// measured slower (the per-group divisions repeat on every lane).
 
 #include <hip/hip_runtime.h>
 
@@ -43,6 +44,19 @@ struct QzArgs {
   long long groups;  // n * (k / G)
   int gpr;           // groups per row
 };
+
+// rint(fl(x / s)) (fl: the correctly rounded quotient) without a division
+// per weight: the hardware reciprocal is within 1 ulp of 1/s, so
+// r = x * (1/s) is within 2.5e-7 |r| of x / s, as is fl(x / s). Where r is
+// farther than 1e-5 + 1e-6 |r| from a half-integer, rint(r) equals
+// rint(fl(x / s)); nearer (rare), the correctly rounded division decides.
+__device__ __forceinline__ float RoundQuotient(float x, float s,
+                                               float inv) {
+  const float r = x * inv;
+  const float c = rintf(r);
+  const float tol = 1e-5f + 1e-6f * fabsf(r);
+  return fabsf(fabsf(r - c) - 0.5f) < tol ? rintf(__fdiv_rn(x, s)) : c;
+}
 
 // One thread per group: its G weights in registers, read as 16-byte
 // vectors.
@@ -72,10 +86,11 @@ __global__ __launch_bounds__(256) void quantize_kernel(QzArgs a) {
 #pragma unroll
     for (int i = 0; i < G; ++i) amax = fmaxf(amax, fabsf(v[i]));
     scale = __fdiv_rn(fmaxf(amax, 1e-12f), 127.f);
+    const float inv = __builtin_amdgcn_rcpf(scale);
 #pragma unroll
     for (int i = 0; i < G; ++i)
       q[i] = static_cast<int>(
-          fminf(fmaxf(rintf(__fdiv_rn(v[i], scale)), -127.f), 127.f));
+          fminf(fmaxf(RoundQuotient(v[i], scale, inv), -127.f), 127.f));
   } else {
     float lo = v[0], hi = v[0];
 #pragma unroll
@@ -89,10 +104,11 @@ __global__ __launch_bounds__(256) void quantize_kernel(QzArgs a) {
       scale = __fdiv_rn(edge, q0);
       offset = edge;
     }
+    const float inv = __builtin_amdgcn_rcpf(scale);
 #pragma unroll
     for (int i = 0; i < G; ++i)
-      q[i] = static_cast<int>(
-          fminf(fmaxf(rintf(__fdiv_rn(v[i] - offset, scale)), 0.f), 15.f));
+      q[i] = static_cast<int>(fminf(
+          fmaxf(RoundQuotient(v[i] - offset, scale, inv), 0.f), 15.f));
   }
   static_cast<ST*>(a.scales)[gid] = from_f32<ST>(scale);
   if constexpr (PACK != QK_PACK_S8_SYM)

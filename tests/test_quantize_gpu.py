@@ -29,6 +29,14 @@ def weights(rng, n, k, group):
         w[0, 3 * group:4 * group] = np.linspace(-1.0, 0.03, group)
         w[0, 4 * group:5 * group] = np.arange(group) % 16 * 0.125
         w[0, 5 * group] = 300.0
+    if n >= 2 and gpr >= 2:
+        # quotients on and a hair off half-integers: 127 (int8) and 15
+        # (int4) steps with weights at k + 1/2 steps and their neighbours
+        t = (np.arange(group) % 126 + 0.5).astype(np.float32)
+        w[1, 0:group] = t / 127.0
+        w[1, group - 1] = 1.0
+        w[1, group:2 * group] = np.nextafter(t, np.float32(0)) / 15.0
+        w[1, 2 * group - 1] = -1.0
     return w
 
 
