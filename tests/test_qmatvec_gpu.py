@@ -348,6 +348,37 @@ def test_qgemm_dma_split_workspace_growth_and_graph(dev, monkeypatch):
         assert torch.equal(out, eager)
 
 
+def test_qgemm_dma_split_on_concurrent_streams(dev, monkeypatch):
+    """Two streams running K-split problems at the same time (each stream
+    has its own workspace and arrival counters): five launches on each,
+    interleaved without synchronization, every output equal bit for bit to
+    the same problem run alone."""
+    rng = np.random.default_rng(9)
+    monkeypatch.setenv("QK_QGEMM_DMA", "2,4")  # 128 x 128 tiles, K split 4
+    probs = []
+    for n in (1024, 2048):
+        dc, ds, db, w, *_ = make_weights(rng, n, 4096, Packing.U32X8, 64)
+        x = O.round_to(rng.standard_normal((100, 4096)),
+                       "bfloat16").astype(np.float32)
+        probs.append((torch.from_numpy(x).to(torch.bfloat16).to(dev),
+                      (dc.to(dev), ds.to(dev), db.to(dev))))
+    alone = [qkern.qmatvec(x, *a) for x, a in probs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[torch.empty_like(alone[i]) for _ in range(5)] for i in range(2)]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    for r in range(5):
+        for i, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                x, a = probs[i]
+                qkern.qmatvec(x, *a, out=outs[i][r])
+    torch.cuda.synchronize()
+    for i in range(2):
+        for o in outs[i]:
+            assert torch.equal(o, alone[i])
+
+
 def test_qmatvec_leading_dims_and_no_bias(dev):
     rng = np.random.default_rng(5)
     dc, ds, _, w, *_ = make_weights(rng, 40, 256, Packing.U32X8, 64,
