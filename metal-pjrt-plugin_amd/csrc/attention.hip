@@ -13,9 +13,11 @@
 // init_cache (qwen3.py:279-291): keys [B, KV, Smax, D], values
 // [B, KV, D, Smax], each with the reduced axis last.
 //
-// attn_split_kernel: one wavefront per (b, h, run of 64-slot chunks); the
-// runs cut the attended window (known only on the device) into a fixed
-// number of parts. Keys and values of a chunk are fetched by LDS DMA as
+// attn_split_kernel: one workgroup of two wavefronts per (b, h, run of
+// 64-slot chunks); the runs cut the attended window (known only on the
+// device) into a fixed number of parts, and each wave takes one 32-slot
+// half of every chunk, with a running softmax of its own that the two
+// merge at the end. Keys and values of a chunk are fetched by LDS DMA as
 // whole contiguous 1 KB pieces into one of two LDS stages (the next chunk
 // is in flight while one is computed) and read back, swizzled against
 // bank conflicts, in the MFMA operand layouts. Scores come from
@@ -25,7 +27,7 @@
 // log2(e)-scaled scores). p goes through a wave-private LDS tile into the
 // A operand of a second MFMA whose B operand is 8 slots of a value row:
 // p is split exactly into two bf16 (or f16) parts, hi + lo, so p.v keeps
-// ~2^-17 relative precision, as f32 arithmetic would. Each wave writes
+// ~2^-17 relative precision, as f32 arithmetic would. Each workgroup writes
 // its partial (max, sum, accumulator row per head) to the workspace.
 // attn_combine_kernel: one workgroup per (b, h, g) and 16 head-dim
 // columns rescales the partials to the common maximum and divides by the
@@ -55,7 +57,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kChunk = 64;        // slots per chunk
-constexpr int kPStride = 64 + 4;  // floats per row of the LDS p tile
+constexpr int kPStride = 32 + 4;  // floats per row of a wave's LDS p tile
+constexpr int kSplitWaves = 2;    // waves per split workgroup
 constexpr int kOut = 0x7FFF0000;  // an offset past every extent
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -125,25 +128,35 @@ struct AttnLds {
   static constexpr int kDmaV = kV / 1024;
   static constexpr int kDma = kDmaK + kDmaV;
   static constexpr int kQ = 16 * D * 2;
+  static constexpr int kDmaQ = kQ / 1024;
   static constexpr int kQOff = 2 * kStage;
   static constexpr int kPOff = kQOff + kQ;
-  static constexpr int kBytes = kPOff + 16 * kPStride * 4;
+  static constexpr int kPTile = 16 * kPStride * 4;  // one per wave
+  static constexpr int kBytes = kPOff + kSplitWaves * kPTile;
+  static_assert(kDmaK % kSplitWaves == 0 && kDmaV % kSplitWaves == 0 &&
+                    kDmaQ % kSplitWaves == 0,
+                "the waves share every DMA group evenly");
+  static_assert(64 * (8 + 4 * (D / 16)) * 4 <= kStage,
+                "the second wave's running state fits in a stage");
   static __device__ __forceinline__ int Swz(int s) {
     return D == 128 ? (s & 15) : ((s >> 1) & 7);
   }
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * kSplitWaves) void attn_split_kernel(
+    AttnArgs a) {
   using M = Mfma<T>;
   using V = typename M::V;
   using L = AttnLds<D>;
   constexpr int kSteps = D / 32;  // 32-wide head-dim steps of a score MFMA
   constexpr int kDB = D / 16;     // 16-wide head-dim blocks of the output
+  constexpr int kDmaW = L::kDma / kSplitWaves;  // DMAs per wave per chunk
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  float* ptile = reinterpret_cast<float*>(smem + L::kPOff);
 
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float* ptile = reinterpret_cast<float*>(smem + L::kPOff + wv * L::kPTile);
   const int bh = blockIdx.y;
   const int w = blockIdx.x;
   const int pos = __builtin_amdgcn_readfirstlane(*a.pos);
@@ -166,34 +179,43 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
 
   // Per-lane DMA offsets within a chunk: key unit p = 64 i + lane is slot
   // p / kUnits, unit (p % kUnits) ^ Swz(slot); value lane covers row
-  // 8 i + lane / 8, unit (lane % 8) ^ ((row >> 1) & 7).
+  // 8 i + lane / 8, unit (lane % 8) ^ ((row >> 1) & 7). Wave wv issues
+  // pieces i = wv * n / kSplitWaves .. of each group of n. The cache is
+  // read once per call: nontemporal.
   auto issue = [&](int chunk) {
     unsigned char* st = smem + (chunk & 1) * L::kStage;
     const int s0 = s_begin + chunk * kChunk;
 #pragma unroll
-    for (int i = 0; i < L::kDmaK; ++i) {
+    for (int ii = 0; ii < L::kDmaK / kSplitWaves; ++ii) {
+      const int i = wv * (L::kDmaK / kSplitWaves) + ii;
       const int p = 64 * i + lane;
       const int sl = p / L::kUnits;
       const int u = (p % L::kUnits) ^ L::Swz(sl);
-      kd.dma(st + 1024 * i, ((s0 + sl) * L::kUnits + u) * 16, 0);
+      kd.dma_nt(st + 1024 * i, ((s0 + sl) * L::kUnits + u) * 16, 0);
     }
 #pragma unroll
-    for (int i = 0; i < L::kDmaV; ++i) {
+    for (int ii = 0; ii < L::kDmaV / kSplitWaves; ++ii) {
+      const int i = wv * (L::kDmaV / kSplitWaves) + ii;
       const int d = 8 * i + lane / 8;
       const int u = (lane % 8) ^ ((d >> 1) & 7);
       const int sv = s0 + 8 * u;
-      vd.dma(st + L::kK + 1024 * i, sv < valid ? (d * a.smax + sv) * 2 : kOut,
-             0);
+      vd.dma_nt(st + L::kK + 1024 * i,
+                sv < valid ? (d * a.smax + sv) * 2 : kOut, 0);
     }
   };
 
   // q first (heads past G read zeros), then the first two chunks.
 #pragma unroll
-  for (int i = 0; i < (L::kQ + 1023) / 1024; ++i)
+  for (int ii = 0; ii < L::kDmaQ / kSplitWaves; ++ii) {
+    const int i = wv * (L::kDmaQ / kSplitWaves) + ii;
     qd.dma(smem + L::kQOff + 1024 * i, (1024 * i + 16 * lane), 0);
+  }
   issue(0);
   if (nchunks > 1) issue(1);
 
+  // Wave wv takes slots 32 wv .. 32 wv + 31 of every chunk: score blocks
+  // j = 2 wv, 2 wv + 1 and p.v step u = wv; each wave keeps a running
+  // softmax of its own, merged with the other's at the end.
   const int r16 = lane & 15, q4 = lane >> 4;
   float m_run[4], l_run[4];
   f32x4 acc[kDB];
@@ -204,10 +226,12 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
   V qf[kSteps];
 
   for (int c = 0; c < nchunks; ++c) {
+    // Chunk c has landed: own DMA by vmcnt, the other wave's by the barrier.
     if (c + 1 < nchunks)
-      __builtin_amdgcn_s_waitcnt(VmcntImm(L::kDma));  // chunk c landed
+      __builtin_amdgcn_s_waitcnt(VmcntImm(kDmaW));
     else
       __builtin_amdgcn_s_waitcnt(VmcntImm(0));
+    __syncthreads();
     const unsigned char* st = smem + (c & 1) * L::kStage;
     const int s0 = s_begin + c * kChunk;
     if (c == 0) {
@@ -222,8 +246,10 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
     }
     // The values of slots [valid, next multiple of 8) were fetched with
     // their unit: zero them (a value there may be anything, even NaN, and
-    // p = 0 would not cancel it).
-    if (valid - s0 < kChunk && (valid & 7) != 0) {
+    // p = 0 would not cancel it). The wave whose half holds the unit does
+    // it; only that wave reads it.
+    if (valid - s0 < kChunk && (valid & 7) != 0 &&
+        ((valid - s0) >> 5) == wv) {
       const int su = (valid - s0) >> 3;  // unit holding slot valid
       unsigned char* vs = const_cast<unsigned char*>(st) + L::kK;
 #pragma unroll
@@ -234,12 +260,12 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
         for (int e = valid & 7; e < 8; ++e) row[e] = from_f32<T>(0.f);
       }
     }
-    // Scores: lane l holds heads 4 q4 + r for slot s0 + 16 j + r16.
-    f32x4 sc[4];
+    // Scores: lane l holds heads 4 q4 + r for slot s0 + 32 wv + 16 j + r16.
+    f32x4 sc[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       sc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int sl = 16 * j + r16;
+      const int sl = 32 * wv + 16 * j + r16;
 #pragma unroll
       for (int t = 0; t < kSteps; ++t) {
         const u32x4 kv = *reinterpret_cast<const u32x4*>(
@@ -251,27 +277,30 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
       for (int r = 0; r < 4; ++r)
         sc[j][r] = in ? sc[j][r] * a.scale_log2 : -__builtin_inff();
     }
-    // Running softmax per head (the lane's rows r).
+    // Running softmax per head (the lane's rows r). The second wave's half
+    // of the last chunk may hold no attended slot: with nothing attended
+    // so far the maximum stays -inf and the shift is taken as 0 (alpha
+    // and p are then 0, not NaN).
     float alpha[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float cm = max16(fmaxf(fmaxf(sc[0][r], sc[1][r]),
-                                   fmaxf(sc[2][r], sc[3][r])));
+      const float cm = max16(fmaxf(sc[0][r], sc[1][r]));
       const float mn = fmaxf(m_run[r], cm);
-      // mn is finite: the chunk's first slot is attended
-      alpha[r] = __builtin_amdgcn_exp2f(m_run[r] - mn);
+      const float sh = mn == -__builtin_inff() ? 0.f : mn;
+      alpha[r] = __builtin_amdgcn_exp2f(m_run[r] - sh);
       m_run[r] = mn;
       float ps = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sc[j][r] = __builtin_amdgcn_exp2f(sc[j][r] - mn);
+      for (int j = 0; j < 2; ++j) {
+        sc[j][r] = __builtin_amdgcn_exp2f(sc[j][r] - sh);
         ps += sc[j][r];
       }
       l_run[r] = l_run[r] * alpha[r] + ps;
     }
-    // p through LDS into the A layout: row = head, K = 8 slots.
+    // p through the wave's LDS tile into the A layout: row = head, K = 8
+    // slots.
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         ptile[(4 * q4 + r) * kPStride + 16 * j + r16] = sc[j][r];
@@ -281,9 +310,8 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
     for (int db = 0; db < kDB; ++db)
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[db][r] *= alpha[r];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const float* pr = ptile + r16 * kPStride + 32 * u + 8 * q4;
+    {
+      const float* pr = ptile + r16 * kPStride + 8 * q4;
       const f32x4 p0 = *reinterpret_cast<const f32x4*>(pr);
       const f32x4 p1 = *reinterpret_cast<const f32x4*>(pr + 4);
       V hi, lo;
@@ -298,19 +326,48 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
       for (int db = 0; db < kDB; ++db) {
         const int d = 16 * db + r16;
         const u32x4 vv = *reinterpret_cast<const u32x4*>(
-            st + L::kK + d * 128 + ((4 * u + q4) ^ ((d >> 1) & 7)) * 16);
+            st + L::kK + d * 128 + ((4 * wv + q4) ^ ((d >> 1) & 7)) * 16);
         const V vbf = __builtin_bit_cast(V, vv);
         acc[db] = M::run(hi, vbf, acc[db]);
         acc[db] = M::run(lo, vbf, acc[db]);
       }
     }
-    // This stage's LDS reads are done before its refill is issued.
+    // Both waves' LDS reads of this stage are done before its refill.
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-    __builtin_amdgcn_wave_barrier();
+    __syncthreads();
     if (c + 2 < nchunks) issue(c + 2);
   }
 
-  // Partial of this wave: heads 4 q4 + r < G.
+  // Merge: the second wave leaves its running state in stage 0 (every DMA
+  // has landed and every read of the stages is done at the last barrier);
+  // the first rescales both to the common maximum (finite: the part's
+  // first slot is attended and lies in the first wave's half).
+  float* xs = reinterpret_cast<float*>(smem) + lane;
+  if (wv == 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      xs[64 * r] = m_run[r];
+      xs[64 * (4 + r)] = l_run[r];
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) xs[64 * (8 + 4 * db + r)] = acc[db][r];
+    }
+  }
+  __syncthreads();
+  if (wv == 1) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float m1 = xs[64 * r];
+    const float mn = fmaxf(m_run[r], m1);
+    const float f0 = __builtin_amdgcn_exp2f(m_run[r] - mn);
+    const float f1 = __builtin_amdgcn_exp2f(m1 - mn);
+    m_run[r] = mn;
+    l_run[r] = l_run[r] * f0 + xs[64 * (4 + r)] * f1;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+      acc[db][r] = acc[db][r] * f0 + xs[64 * (8 + 4 * db + r)] * f1;
+  }
+
+  // Partial of this workgroup: heads 4 q4 + r < G.
   const long long pidx = static_cast<long long>(bh) * a.parts + w;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -411,7 +468,8 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(
 
 template <typename T, int D>
 qk_status Launch(const AttnArgs& a, int bkv, hipStream_t st) {
-  attn_split_kernel<T, D><<<dim3(a.parts, bkv), 64, AttnLds<D>::kBytes, st>>>(a);
+  attn_split_kernel<T, D><<<dim3(a.parts, bkv), 64 * kSplitWaves,
+                            AttnLds<D>::kBytes, st>>>(a);
   if (qk_status s = PostLaunch("attn_split_kernel"); s != QK_OK) return s;
   attn_combine_kernel<T, D>
       <<<dim3(bkv * a.g, D / kCombineCols), kCombineThreads, 0, st>>>(a);

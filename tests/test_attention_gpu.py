@@ -104,10 +104,12 @@ def test_decode_attention_short_prefix_of_long_window(dev):
         check_attention(got, q, k, v, pos, 128 ** -0.5, 0)
 
 
-@pytest.mark.parametrize("pos", [500, 503, 511])
+@pytest.mark.parametrize("pos", [467, 500, 503, 511])
 def test_decode_attention_slots_past_position_take_no_part(dev, pos):
     # NaN keys and values in every slot past the position (also inside the
-    # last 8-slot unit the values are fetched in) leave the output finite
+    # last 8-slot unit the values are fetched in, in either half of the
+    # last chunk: 467 and 500 end in its first and second half) leave the
+    # output finite
     rng = np.random.default_rng(10 + pos)
     q, k, v = make_case(rng, 2, 2, 4, 128, 1024, "bfloat16")
     kp, vp = k.copy(), v.copy()
