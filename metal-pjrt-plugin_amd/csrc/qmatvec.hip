@@ -345,103 +345,113 @@ __global__ __launch_bounds__(kWaves * 64) void qmv_generic_kernel(QmvArgs a) {
   }
 }
 
-// Dequantize: one thread per 16-byte chunk of codes.
+// Dequantize: one thread per unit of codes that decodes to runs of 8
+// consecutive values of a row: a 4-byte word of 8 int4 codes (U32X8), 8
+// int8 codes, or 8 bytes of half-split int4 codes (runs at j and
+// j + group / 2). Consecutive lanes load consecutive code bytes and store
+// consecutive 16-byte runs (32 for f32 output), so both sides coalesce. A
+// run never crosses a group (groups of 32, 64, 128).
 // w = f32(q) * f32(scale) rounded, + f32(bias) rounded, then rounded once
 // more to the output type (no fused multiply-add).
-template <int PACK, typename OT, int CPT>
-__global__ void dequant_kernel(QmvArgs a, long long total_chunks) {
-  // CPT consecutive chunks of one row per thread (one measures faster
-  // than four for a gather of scattered rows).
-  const long long t0 = (static_cast<long long>(blockIdx.x) * blockDim.x +
-                        threadIdx.x) * CPT;
-  if (t0 >= total_chunks) return;
-  constexpr bool kInt4 = PACK == QK_PACK_U32X8 || PACK == QK_PACK_BYTE_HALFSPLIT;
-  constexpr int kCodes = kInt4 ? 32 : 16;
-  const int cpr = a.row_bytes / 16;
-  const int orow = static_cast<int>(t0 / cpr);
-  // An embedding gather reads table row gather[orow], clamped into range
-  // (as a JAX gather clamps out-of-range indices).
-  const int row = a.gather == nullptr
-                      ? orow
-                      : min(max(a.gather[orow], 0), a.n - 1);
-  const int c0 = static_cast<int>(t0 % cpr);
+template <int PACK>
+struct DqUnit {
+  static constexpr int kBytes = PACK == QK_PACK_U32X8 ? 4 : 8;
+  static constexpr int kRuns = PACK == QK_PACK_BYTE_HALFSPLIT ? 2 : 1;
+};
+
+template <int PACK, typename OT, int UPT>
+__global__ __launch_bounds__(256) void dequant_kernel(QmvArgs a,
+                                                     long long total_units) {
+  using U = DqUnit<PACK>;
+  // Units j * 256 + threadIdx.x of the block's run of 256 UPT (all loads
+  // first, then the stores).
+  const long long base = static_cast<long long>(blockIdx.x) * 256 * UPT;
+  const int upr = a.row_bytes / U::kBytes;
   const int hg = a.group / 2;
-  u32x4 wv[CPT];
-  float sv[CPT], bv[CPT];
-  int kbv[CPT];
+  uint32_t w[UPT][2];
+  float s[UPT], b[UPT];
+  int orow[UPT], kb[UPT];
 #pragma unroll
-  for (int j = 0; j < CPT; ++j) {
-    const int c = c0 + j;
-    int kb, grp;
+  for (int j = 0; j < UPT; ++j) {
+    const long long t = min(base + j * 256 + threadIdx.x, total_units - 1);
+    orow[j] = static_cast<int>(t / upr);
+    // An embedding gather reads table row gather[orow], clamped into
+    // range (as a JAX gather clamps out-of-range indices).
+    const int row = a.gather == nullptr
+                        ? orow[j]
+                        : min(max(a.gather[orow[j]], 0), a.n - 1);
+    const int byte0 = static_cast<int>(t % upr) * U::kBytes;
+    int grp;
     if (PACK == QK_PACK_BYTE_HALFSPLIT) {
-      const int byte0 = c * 16;
       grp = byte0 / hg;
-      kb = grp * a.group + byte0 % hg;
+      kb[j] = grp * a.group + byte0 % hg;
     } else {
-      kb = c * kCodes;
-      grp = kb / a.group;
+      kb[j] = PACK == QK_PACK_U32X8 ? 2 * byte0 : byte0;
+      grp = kb[j] / a.group;
     }
-    kbv[j] = kb;
-    wv[j] = *reinterpret_cast<const u32x4*>(
-        a.codes + static_cast<long long>(row) * a.row_bytes + c * 16);
+    const unsigned char* src =
+        a.codes + static_cast<long long>(row) * a.row_bytes + byte0;
+    if (U::kBytes == 4) {
+      w[j][0] = *reinterpret_cast<const uint32_t*>(src);
+      w[j][1] = 0;
+    } else {
+      const uint2 d = *reinterpret_cast<const uint2*>(src);
+      w[j][0] = d.x;
+      w[j][1] = d.y;
+    }
     const long long gi = static_cast<long long>(row) * (a.k / a.group) + grp;
-    sv[j] = load_any(a.scales, gi, a.sdt);
-    bv[j] = a.has_bias ? load_any(a.biases, gi, a.bdt) : 0.f;
+    s[j] = load_any(a.scales, gi, a.sdt);
+    b[j] = a.has_bias ? load_any(a.biases, gi, a.bdt) : 0.f;
   }
 #pragma unroll
-  for (int j = 0; j < CPT; ++j) {
-  const u32x4 w = wv[j];
-  const float s = sv[j], b = bv[j];
-  OT* out = static_cast<OT*>(a.y) + static_cast<long long>(orow) * a.k + kbv[j];
-  // The chunk's values by output offset from kb: 32 (int4) or 16 (int8)
-  // consecutive elements; half-split int4: 16 at 0 and 16 at hg.
-  float v[kCodes];
+  for (int j = 0; j < UPT; ++j) {
+    if (base + j * 256 + threadIdx.x >= total_units) break;
+    // v[8 r + e]: element e of run r.
+    float v[8 * U::kRuns];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t word = w[i];
-    if (kInt4) {
-#pragma unroll
-      for (int nib = 0; nib < 8; ++nib) {
-        const int off = PACK == QK_PACK_U32X8
-                            ? 8 * i + nib
-                            : ((nib & 1) ? 16 : 0) + 4 * i + (nib >> 1);
-        const float q = static_cast<float>((word >> (4 * nib)) & 15u);
-        v[off] = __fadd_rn(__fmul_rn(q, s), b);
+    for (int e = 0; e < 8; ++e) {
+      float q0, q1 = 0.f;
+      if (PACK == QK_PACK_U32X8) {
+        q0 = static_cast<float>((w[j][0] >> (4 * e)) & 15u);
+      } else {
+        const uint32_t byte = (w[j][e >> 2] >> (8 * (e & 3))) & 255u;
+        if (PACK == QK_PACK_BYTE_HALFSPLIT) {
+          q0 = static_cast<float>(byte & 15u);
+          q1 = static_cast<float>(byte >> 4);
+        } else if (PACK == QK_PACK_S8_SYM) {
+          q0 = static_cast<float>(static_cast<int8_t>(byte));
+        } else {
+          q0 = static_cast<float>(byte);
+        }
       }
-    } else {
+      v[e] = __fadd_rn(__fmul_rn(q0, s[j]), b[j]);
+      if (U::kRuns == 2) v[8 + e] = __fadd_rn(__fmul_rn(q1, s[j]), b[j]);
+    }
+    OT* out =
+        static_cast<OT*>(a.y) + static_cast<long long>(orow[j]) * a.k + kb[j];
 #pragma unroll
-      for (int bt = 0; bt < 4; ++bt) {
-        float q;
-        if (PACK == QK_PACK_S8_SYM)
-          q = static_cast<float>(static_cast<int8_t>(word >> (8 * bt)));
-        else
-          q = static_cast<float>((word >> (8 * bt)) & 255u);
-        v[4 * i + bt] = __fadd_rn(__fmul_rn(q, s), b);
+    for (int r = 0; r < U::kRuns; ++r) {
+      OT* dst = out + r * hg;
+      if (a.out_vec) {
+        // Whole 16-byte stores: every run starts at a multiple of 8
+        // elements.
+        constexpr int kPer = 16 / sizeof(OT);
+#pragma unroll
+        for (int q = 0; q < 8 / kPer; ++q) {
+          union {
+            u32x4 u;
+            OT e[kPer];
+          } o;
+#pragma unroll
+          for (int e = 0; e < kPer; ++e)
+            o.e[e] = from_f32<OT>(v[8 * r + kPer * q + e]);
+          *reinterpret_cast<u32x4*>(dst + kPer * q) = o.u;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[e] = from_f32<OT>(v[8 * r + e]);
       }
     }
-  }
-  // Runs of 16 values: whole 16-byte stores when the output allows them
-  // (a.out_vec), else element by element.
-#pragma unroll
-  for (int r = 0; r < kCodes / 16; ++r) {
-    OT* dst = out + (PACK == QK_PACK_BYTE_HALFSPLIT ? r * hg : r * 16);
-    if (a.out_vec) {
-      constexpr int kPer = 16 / sizeof(OT);
-#pragma unroll
-      for (int q = 0; q < 16 / kPer; ++q) {
-        union {
-          u32x4 u;
-          OT e[kPer];
-        } o;
-#pragma unroll
-        for (int e = 0; e < kPer; ++e) o.e[e] = from_f32<OT>(v[16 * r + kPer * q + e]);
-        *reinterpret_cast<u32x4*>(dst + kPer * q) = o.u;
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) dst[e] = from_f32<OT>(v[16 * r + e]);
-    }
-  }
   }
 }
 
@@ -1495,26 +1505,34 @@ qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream) {
 qk_status LaunchDequantize(const QuantProblem& p, hipStream_t stream) {
   if (qk_status s = CheckLimits(p); s != QK_OK) return s;
   QmvArgs a = MakeArgs(p);
-  // Every 16-value run starts at a multiple of 8 elements of its row.
+  // Every 8-value run starts at a multiple of 8 elements of its row.
   a.out_vec = reinterpret_cast<uintptr_t>(p.y) % 16 == 0 &&
-              (p.k * DTypeSize(p.y_dtype)) % 16 == 0 && p.group % 16 == 0;
-  const long long chunks =
-      (p.rows != nullptr ? p.rows_n : p.n) * (a.row_bytes / 16);
-  dim3 block(256), grid(static_cast<unsigned>((chunks + 255) / 256));
+              (p.k * DTypeSize(p.y_dtype)) % 16 == 0;
+  const long long rows = p.rows != nullptr ? p.rows_n : p.n;
+  const int unit = p.packing == QK_PACK_U32X8 ? 4 : 8;
+  const long long units = rows * (a.row_bytes / unit);
+  if (units == 0) return QK_OK;  // (the kernel clamps into [0, units))
+  // Units per thread: 1 (2 measured level for the int4 embedding gather).
+  constexpr int kUpt = 1;
+  dim3 block(256), grid(static_cast<unsigned>((units + 256 * kUpt - 1) /
+                                             (256 * kUpt)));
+  if (units / (256 * kUpt) >= 0x7fffffffLL) {
+    return Fail(QK_UNIMPLEMENTED, "qkern: dequantize grid too large");
+  }
 #define QK_DQ(OT)                                                              \
   switch (p.packing) {                                                         \
     case QK_PACK_U32X8:                                                        \
-      dequant_kernel<QK_PACK_U32X8, OT, 1><<<grid, block, 0, stream>>>(a, chunks); \
+      dequant_kernel<QK_PACK_U32X8, OT, kUpt><<<grid, block, 0, stream>>>(a, units); \
       break;                                                                   \
     case QK_PACK_BYTE_HALFSPLIT:                                               \
-      dequant_kernel<QK_PACK_BYTE_HALFSPLIT, OT, 1>                            \
-          <<<grid, block, 0, stream>>>(a, chunks);                             \
+      dequant_kernel<QK_PACK_BYTE_HALFSPLIT, OT, kUpt>                         \
+          <<<grid, block, 0, stream>>>(a, units);                              \
       break;                                                                   \
     case QK_PACK_U8:                                                           \
-      dequant_kernel<QK_PACK_U8, OT, 1><<<grid, block, 0, stream>>>(a, chunks);    \
+      dequant_kernel<QK_PACK_U8, OT, kUpt><<<grid, block, 0, stream>>>(a, units);    \
       break;                                                                   \
     default:                                                                   \
-      dequant_kernel<QK_PACK_S8_SYM, OT, 1><<<grid, block, 0, stream>>>(a, chunks); \
+      dequant_kernel<QK_PACK_S8_SYM, OT, kUpt><<<grid, block, 0, stream>>>(a, units); \
   }
   if (p.y_dtype == QK_BF16) {
     QK_DQ(bf16)
