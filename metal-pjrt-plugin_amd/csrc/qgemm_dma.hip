@@ -97,12 +97,15 @@ qk_status LaunchQGemmDma(const QuantProblem& p, hipStream_t stream) {
   // split that keeps one workgroup per CU (each partial beyond the first
   // costs the last workgroup a memory round trip): 128 x 12288 x 4096 split
   // 2 (31 us), 128 x 4096 x 4096 split 4 (24 us), 512 x 4096 x 12288
-  // split 2 (72 us).
+  // split 2 (72 us). 256-row tiles only for more than 128 rows: at M <= 128
+  // half their rows are padding (128 x 151936 x 4096, where N is not a
+  // multiple of 256: 337 us with 256 x 128 tiles, 273 with 128 x 128;
+  // 128 x 32768 x 4096: 82 against 63).
   const long long fill = static_cast<long long>(cus) * 5;
   int best_i = -1, best_split = 1;
   if (valid(1, 1) && tiles_of(1) * 8 >= fill) {
     best_i = 1;
-  } else if (valid(0, 1) && tiles_of(0) * 8 >= fill) {
+  } else if (valid(0, 1) && g.m > 128 && tiles_of(0) * 8 >= fill) {
     best_i = 0;
   } else if (valid(2, 1)) {
     best_i = 2;

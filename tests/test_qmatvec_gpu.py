@@ -548,6 +548,14 @@ def test_config_int4(dev, nk, m):
     run_config_int4(dev, m, n, k, config_rows(m), seed={1: 1}.get(m, 2))
 
 
+def test_config_int4_lm_head_128_rows(dev):
+    # 128 rows against the lm_head: N = 151936 is not a multiple of 256, so
+    # the GEMM runs 128 x 128 tiles (no 256-row tile, half of whose rows
+    # would be padding); rows from the start, middle and end of the tile
+    run_config_int4(dev, 128, 151936, 4096, np.r_[0:8, 60:68, 120:128],
+                    seed=4)
+
+
 @pytest.mark.parametrize("m", [1, 8, 128])
 def test_config_int8_affine(dev, m):
     n, k = 12288, 4096
