@@ -460,6 +460,26 @@ def test_dequantize_bit_exact(dev, packing, odt):
         assert np.array_equal(got, want), (n, k, group)
 
 
+@pytest.mark.parametrize("packing", list(Packing))
+@pytest.mark.parametrize("odt", ["bfloat16", "float32"])
+def test_dequantize_into_unaligned_output(dev, packing, odt):
+    # an output that is not 16-byte aligned takes element-wise stores: the
+    # same bits as the 16-byte stores into an aligned output
+    rng = np.random.default_rng(12)
+    n, k, group = 9, 256, 32
+    dc, ds, db, *_ = make_weights(rng, n, k, packing, group)
+    args = (dc.to(dev), ds.to(dev), None if db is None else db.to(dev))
+    kw = dict(k=k, packing=packing, group_size=group, dtype=TORCH[odt])
+    want = qkern.dequantize(*args, **kw)
+    buf = torch.zeros(n * k + 1, dtype=TORCH[odt], device=dev)
+    out = buf[1:].view(n, k)
+    qkern.dequantize(*args, out=out, **kw)
+    torch.cuda.synchronize()
+    assert out.data_ptr() % 16 != 0
+    assert torch.equal(out, want)
+    assert buf[0].item() == 0
+
+
 def test_dequantize_f32_scale_rounding_unfused(dev):
     # f32 scales: q*s must round in f32 before + b (no fused multiply-add).
     n, k = 4, 64
