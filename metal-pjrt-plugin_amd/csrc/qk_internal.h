@@ -134,6 +134,10 @@ qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream);
 // int8, bf16, group 64.
 bool QSkinnyApplies(const QuantProblem& p);
 qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream);
+// int4, bf16, group 64, 1..16 rows, K a multiple of 512 up to 4096
+// (qstream.hip).
+bool QStreamApplies(const QuantProblem& p);
+qk_status LaunchQStream(const QuantProblem& p, hipStream_t stream);
 
 // Quantized matmul for up to 128 rows of x (qmid.hip): int4 u32x8 or
 // int8, bf16, group 64, K a multiple of 256.

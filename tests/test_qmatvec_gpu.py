@@ -134,9 +134,9 @@ def test_qmatvec_few_rows(dev, mnk, packing):
     offsets, elementwise against the float64 oracle. For int4 and at most
     16 rows: the streamed kernel with 16, 32 and 48 weight rows per
     workgroup (N = 4096, 6000, 9000; the last two with a partly filled
-    workgroup), its persistent form where 48-row blocks outnumber the CUs
-    and K <= 4096 (N = 12400, 12500; K of 4 and 16 items of four groups)
-    and the register-staged kernel beyond (K = 5120); for
+    workgroup), the streamed MFMA kernel with x in registers where 48-row
+    blocks outnumber the CUs and K <= 4096 (N = 12400, 12500) and the
+    register-staged kernel beyond (K = 5120); for
     int4 and 17..32 rows the streamed kernel with two row blocks of x
     (M = 32, 27)."""
     m, n, k = mnk
@@ -435,6 +435,31 @@ def test_qmatvec_reference_quantizer_end_to_end(dev):
     want8 = O.matvec_int8_reference_form(x, q8.reshape(96, -1, 64),
                                          s8b.reshape(96, -1, 1))
     assert O.rel_fro(y8.float().cpu().numpy(), want8) <= 1e-2
+
+
+@pytest.mark.parametrize("mnk", [(5, 16400, 512), (16, 12400, 1024),
+                                 (9, 20000, 2048), (16, 13000, 4096),
+                                 (12, 18990, 4096)])
+def test_qmatvec_wide_few_rows_both_paths(dev, mnk, monkeypatch):
+    """int4, 5..16 rows, N above 48 rows per CU: the streamed MFMA kernel
+    with x in registers (K / 512 waves per 16-row block: 1, 2, 4 and 8;
+    ragged last block) and the persistent producer / consumer kernel it
+    replaced there (QK_QSTREAM=0), each against the float64 oracle."""
+    m, n, k = mnk
+    rng = np.random.default_rng(n + k)
+    for has_bias in (True, False):
+        dc, ds, db, w, *_ = make_weights(rng, n, k, Packing.U32X8, 64,
+                                         has_bias=has_bias)
+        x = O.round_to(rng.standard_normal((m, k)), "bfloat16").astype(
+            np.float32)
+        args = (torch.from_numpy(x).to(torch.bfloat16).to(dev), dc.to(dev),
+                ds.to(dev), None if db is None else db.to(dev))
+        for off in ("1", "0"):
+            monkeypatch.setenv("QK_QSTREAM", off)
+            y = qkern.qmatvec(*args)
+            torch.cuda.synchronize()
+            check_matvec(y.float().cpu().numpy().astype(np.float64), x, w)
+        monkeypatch.delenv("QK_QSTREAM")
 
 
 @pytest.mark.parametrize("packing", list(Packing))
