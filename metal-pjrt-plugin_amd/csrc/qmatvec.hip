@@ -1447,16 +1447,17 @@ qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream) {
   // (tuning; read at every call).
   const char* dmv = std::getenv("QK_QGEMM_DMA_MIN_M");
   const int dma_min_m = dmv == nullptr ? 33 : std::atoi(dmv);
-  // QK_QSTREAM=0 turns the streamed MFMA kernel off (tuning; read at every
-  // call).
+  // QK_QSTREAM=0 turns the streamed MFMA kernel off, =2 takes it wherever
+  // it applies (tuning; read at every call).
   const char* qsv = std::getenv("QK_QSTREAM");
   const bool qstream = qsv == nullptr || *qsv != '0';
+  const bool qstream_all = qsv != nullptr && *qsv == '2';
   // The streamed MFMA kernel with x in registers where 48-row blocks
   // outnumber the CUs (int4, <= 16 rows, K <= 4096: the lm_head, 82
   // against 118 us at M = 16; 16384 x 4096 17 against 26); below, the
   // skinny kernels' single round is faster (12288 x 4096 12 against 15).
   if (m > 4 && qstream && QStreamApplies(p) &&
-      p.n > int64_t{48} * DeviceComputeUnits())
+      (qstream_all || p.n > int64_t{48} * DeviceComputeUnits()))
     return LaunchQStream(p, stream);
   if (m > 4 && QSkinnyApplies(p)) return LaunchQSkinny(p, stream);
   // 33..64 rows: the K-split dequantizing kernel where it applies (int4
