@@ -137,6 +137,8 @@ qk_status LaunchQSkinny(const QuantProblem& p, hipStream_t stream);
 // int4, bf16, group 64, 1..16 rows, K a multiple of 512 up to 4096
 // (qstream.hip).
 bool QStreamApplies(const QuantProblem& p);
+// Row-block rounds each of its waves runs on `cus` CUs.
+int QStreamRounds(const QuantProblem& p, int cus);
 qk_status LaunchQStream(const QuantProblem& p, hipStream_t stream);
 
 // Quantized matmul for up to 128 rows of x (qmid.hip): int4 u32x8 or

@@ -1452,12 +1452,13 @@ qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream) {
   const char* qsv = std::getenv("QK_QSTREAM");
   const bool qstream = qsv == nullptr || *qsv != '0';
   const bool qstream_all = qsv != nullptr && *qsv == '2';
-  // The streamed MFMA kernel with x in registers where 48-row blocks
-  // outnumber the CUs (int4, <= 16 rows, K <= 4096: the lm_head, 82
-  // against 118 us at M = 16; 16384 x 4096 17 against 26); below, the
-  // skinny kernels' single round is faster (12288 x 4096 12 against 15).
+  // The streamed MFMA kernel with x in registers where each of its waves
+  // runs at least three row-block rounds (int4, <= 16 rows, K <= 4096: the
+  // lm_head, 74 against 118 us at M = 16; 12288 x 4096 11 against 12);
+  // with fewer, reading all of x per workgroup costs more than the skinny
+  // kernels' single round (8192 x 4096 10 against 8).
   if (m > 4 && qstream && QStreamApplies(p) &&
-      (qstream_all || p.n > int64_t{48} * DeviceComputeUnits()))
+      (qstream_all || QStreamRounds(p, DeviceComputeUnits()) >= 3))
     return LaunchQStream(p, stream);
   if (m > 4 && QSkinnyApplies(p)) return LaunchQSkinny(p, stream);
   // 33..64 rows: the K-split dequantizing kernel where it applies (int4

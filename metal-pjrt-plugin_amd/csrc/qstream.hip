@@ -336,6 +336,27 @@ bool QStreamApplies(const QuantProblem& p) {
          (!p.has_bias || reinterpret_cast<uintptr_t>(p.biases) % 16 == 0);
 }
 
+namespace {
+struct QsGrid {
+  int ks, grid, rounds;
+};
+QsGrid QStreamGrid(const QuantProblem& p, int cus) {
+  QsGrid g;
+  g.ks = static_cast<int>(p.k / kQsSliceK);  // waves per row block
+  const int rpw = kQsWaves / g.ks;
+  const int64_t rowblocks = (p.n + 15) / 16;
+  g.grid = static_cast<int>(std::max<int64_t>(
+      1, std::min<int64_t>(cus, (rowblocks + rpw - 1) / rpw)));
+  g.rounds = static_cast<int>((rowblocks + int64_t{g.grid} * rpw - 1) /
+                              (int64_t{g.grid} * rpw));
+  return g;
+}
+}  // namespace
+
+int QStreamRounds(const QuantProblem& p, int cus) {
+  return QStreamGrid(p, cus).rounds;
+}
+
 qk_status LaunchQStream(const QuantProblem& p, hipStream_t stream) {
   QsArgs a;
   a.x = p.x;
@@ -348,24 +369,30 @@ qk_status LaunchQStream(const QuantProblem& p, hipStream_t stream) {
   a.k = static_cast<int>(p.k);
   a.has_bias = p.has_bias ? 1 : 0;
   a.rowblocks = static_cast<int>((p.n + 15) / 16);
-  const int cus = DeviceComputeUnits();
-  const int ks = a.k / kQsSliceK;  // waves per row block
-  const int rpw = kQsWaves / ks;
-  const int grid = std::max(1, std::min(cus, (a.rowblocks + rpw - 1) / rpw));
-  a.rounds = (a.rowblocks + grid * rpw - 1) / (grid * rpw);
-  constexpr int PD = 4;
-  switch (ks) {
+  const QsGrid g = QStreamGrid(p, DeviceComputeUnits());
+  a.rounds = g.rounds;
+  // Rounds in flight per wave: one for short runs (a deeper ring only adds
+  // padding and registers: 12288 x 4096 11.2 against 13.2 us), four for
+  // long ones (the lm_head 74 against 82 us).
+  const bool deep = g.rounds > 8;
+  auto go = [&](auto k1, auto k4) {
+    if (deep)
+      k4<<<g.grid, kQsWaves * 64, 0, stream>>>(a);
+    else
+      k1<<<g.grid, kQsWaves * 64, 0, stream>>>(a);
+  };
+  switch (g.ks) {
     case 1:
-      qmm_stream_kernel<1, PD><<<grid, kQsWaves * 64, 0, stream>>>(a);
+      go(qmm_stream_kernel<1, 1>, qmm_stream_kernel<1, 4>);
       break;
     case 2:
-      qmm_stream_kernel<2, PD><<<grid, kQsWaves * 64, 0, stream>>>(a);
+      go(qmm_stream_kernel<2, 1>, qmm_stream_kernel<2, 4>);
       break;
     case 4:
-      qmm_stream_kernel<4, PD><<<grid, kQsWaves * 64, 0, stream>>>(a);
+      go(qmm_stream_kernel<4, 1>, qmm_stream_kernel<4, 4>);
       break;
     case 8:
-      qmm_stream_kernel<8, PD><<<grid, kQsWaves * 64, 0, stream>>>(a);
+      go(qmm_stream_kernel<8, 1>, qmm_stream_kernel<8, 4>);
       break;
     default:
       return Fail(QK_INTERNAL, "qkern: qmm_stream slice count");

@@ -439,12 +439,13 @@ def test_qmatvec_reference_quantizer_end_to_end(dev):
 
 @pytest.mark.parametrize("mnk", [(5, 16400, 512), (16, 12400, 1024),
                                  (9, 20000, 2048), (16, 13000, 4096),
-                                 (12, 18990, 4096)])
+                                 (12, 18990, 4096), (16, 40000, 4096)])
 def test_qmatvec_wide_few_rows_both_paths(dev, mnk, monkeypatch):
     """int4, 5..16 rows, N above 48 rows per CU: the streamed MFMA kernel
     with x in registers (K / 512 waves per 16-row block: 1, 2, 4 and 8;
-    ragged last block) and the persistent producer / consumer kernel it
-    replaced there (QK_QSTREAM=0), each against the float64 oracle."""
+    one ring slot for short runs, four for long ones; ragged last block)
+    and the skinny kernels it replaces on long runs (QK_QSTREAM=0), each
+    against the float64 oracle."""
     m, n, k = mnk
     rng = np.random.default_rng(n + k)
     for has_bias in (True, False):
@@ -454,7 +455,7 @@ def test_qmatvec_wide_few_rows_both_paths(dev, mnk, monkeypatch):
             np.float32)
         args = (torch.from_numpy(x).to(torch.bfloat16).to(dev), dc.to(dev),
                 ds.to(dev), None if db is None else db.to(dev))
-        for off in ("1", "0"):
+        for off in ("2", "0"):  # the streamed kernel forced, then off
             monkeypatch.setenv("QK_QSTREAM", off)
             y = qkern.qmatvec(*args)
             torch.cuda.synchronize()
