@@ -58,13 +58,16 @@ def test_host_argument_errors_are_not_sticky(dev):
 
 @pytest.mark.parametrize("m,n", [(16, 4096), (64, 4096), (8, 151936)],
                          ids=["ws", "wsmid", "wsp"])
-def test_wait_timeout_is_an_error_not_wrong_values(dev, m, n):
+def test_wait_timeout_is_an_error_not_wrong_values(dev, m, n, monkeypatch):
     # The producer / consumer kernels (rows 5..16, 33..128 and the
     # persistent lm_head form) wait on LDS flags with a bounded spin. A wait
     # that gives up must surface as the sticky device error with NaN
     # outputs, never as plausible values. QK_SPIN_LIMIT=0 makes every wait
     # give up at once from the host side: no wait is left unbounded and
-    # every kernel still ends normally.
+    # every kernel still ends normally. QK_QSTREAM=0 keeps the lm_head
+    # shape on the persistent kernel (the streamed kernel that serves it
+    # otherwise has no waits).
+    monkeypatch.setenv("QK_QSTREAM", "0")
     k = 4096
     g = torch.Generator().manual_seed(7)
     x = torch.randn(m, k, generator=g).to(torch.bfloat16).to(dev)
