@@ -275,7 +275,7 @@ def test_activation_special_values(dev, epilogue):
 def test_split_k_kernel(dev, ta, tb):
     """Few output tiles and a long K run the split-K kernel (each wave a
     quarter of K, reduced through LDS): ragged M/N/K, all transposes."""
-    plan = run_case(dev, 64, 512, 2048, ta=ta, tb=tb)
+    plan = run_case(dev, 80, 512, 2048, ta=ta, tb=tb)
     assert "gemm_splitk4" in plan.describe()
     plan = run_case(dev, 100, 260, 1500, ta=ta, tb=tb, tin="float16",
                     beta=0.5)
@@ -285,8 +285,12 @@ def test_split_k_kernel(dev, ta, tb):
 @pytest.mark.parametrize("ta", [False, True])
 @pytest.mark.parametrize("tb", [False, True])
 def test_split_k_kernel_few_rows(dev, ta, tb):
-    """At most 32 rows (or columns): 32x32 tiles, eight waves over K."""
+    """At most 64 rows (or columns): 32x32 tiles, eight waves over K."""
     plan = run_case(dev, 16, 700, 2048, ta=ta, tb=tb)
+    assert "gemm_splitk8" in plan.describe()
+    plan = run_case(dev, 64, 512, 2048, ta=ta, tb=tb)
+    assert "gemm_splitk8" in plan.describe()
+    plan = run_case(dev, 61, 1030, 1024, ta=ta, tb=tb, tin="float16")
     assert "gemm_splitk8" in plan.describe()
     plan = run_case(dev, 300, 5, 1100, ta=ta, tb=tb, tin="float16",
                     epilogue=Epilogue.kBiasThenSILU)
@@ -334,6 +338,9 @@ def test_split_k_kernel_epilogues(dev):
                     separate_c=True, beta=1.0)
     assert "gemm_splitk8" in plan.describe()
     plan = run_case(dev, 48, 384, 1024, batch=3, pad=8, tout="float32",
+                    epilogue=Epilogue.kBiasThenGELU)
+    assert "gemm_splitk8" in plan.describe()
+    plan = run_case(dev, 96, 384, 1024, batch=3, pad=8, tout="float32",
                     epilogue=Epilogue.kBiasThenGELU)
     assert "gemm_splitk4" in plan.describe()
 
