@@ -288,6 +288,19 @@ qk_status DispatchFastM(const GemmArgs& g, int batch, bool ta, bool tb,
   return PostLaunch(name);
 }
 
+// 32x32 tiles with sixteen waves over K, A [M][K] and B [N][K] only (both
+// K-contiguous: the sixteen wave-private stages of the other layouts do not
+// fit the LDS).
+template <typename T>
+qk_status DispatchSplitKNT16(const GemmArgs& g, int batch, hipStream_t stream,
+                             const char* name) {
+  dim3 grid(g.tiles_m * g.tiles_n, batch);
+  using AN = DenseA<T, 32, 64, 64, true>;
+  using BT_ = DenseB<T, 32, 64, 64, true>;
+  gemm_splitk_kernel<T, 32, 32, 64, 16, AN, BT_><<<grid, 1024, 0, stream>>>(g);
+  return PostLaunch(name);
+}
+
 // M a multiple of 256: the kernel without row checks; otherwise the last
 // M tile is partly filled.
 template <typename T, int BN, int NW = 4>
@@ -390,9 +403,10 @@ constexpr HalfTile kHalfTiles[] = {
     {64, 64, 2, 2},    // 8: split-K, four waves each a quarter of K
     {32, 32, 2, 4},    // 9: split-K for up to 32 rows, eight waves
     {256, 192, 4, 2},  // 10: interior-tile LDS-DMA kernel, 8 waves of 64 x 96
+    {32, 32, 2, 8},    // 11: split-K for up to 64 rows, sixteen waves
 };
 constexpr int kFastTile256 = 6, kFastTile128 = 7, kSplitK = 8, kSplitK32 = 9,
-              kFastTile192 = 10;
+              kFastTile192 = 10, kSplitK32W16 = 11;
 // f32 problems on the split-bf16 kernel, and few-row f16/bf16 problems on
 // the wide gemv (tile indices below 0: not kHalfTiles entries).
 constexpr int kF32x3Tile128 = -2, kF32x3Tile64 = -3, kGemvTile = -4;
@@ -470,6 +484,8 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
         (t == kFastTile192 && !FastApplies(p, 192)) ||
         (t == kFastTile128 && !FastApplies(p, 128)))
       t = -1;
+    if (t == kSplitK32W16 && (p.a.transpose || !p.b.transpose))
+      t = kSplitK32;
     const int cus = DeviceComputeUnits();
     if (t < 0) {
       // One 256-row tile per CU: the fewest rounds of resident tiles,
@@ -490,13 +506,19 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
     }
     // At most eight rows of x against NT weights: the wide gemv
     // (bandwidth-bound on the weights).
-    if (t < 0 && GemvApplies(p)) t = kGemvTile;
     // Few 64x64 tiles and a long K: split K over the waves of each tile
     // (32x32 tiles and eight waves for at most 64 rows or columns: at 33..64
     // rows they give twice the workgroups over the same weight columns;
-    // 28 x [64, 1024] x [1024, 6144]^T 312 -> 229 us on MI355X).
-    if (t == -1 && tiles(64, 64) < 2 * cus && CeilDiv(p.k, 64) >= 16)
-      t = std::min(p.m, p.n) <= 64 ? kSplitK32 : kSplitK;
+    // 28 x [64, 1024] x [1024, 6144]^T 312 -> 229 us on MI355X). At most 16
+    // rows against NT weights: sixteen waves, twice the loads in flight per
+    // workgroup (M = 16 184 -> 168 us; M = 8 173 us against the gemv's 200).
+    const bool splitk = tiles(64, 64) < 2 * cus && CeilDiv(p.k, 64) >= 16;
+    const bool nt16 = splitk && p.m <= 16 && !p.a.transpose && p.b.transpose;
+    if (t < 0 && GemvApplies(p) && !(nt16 && p.m > 6)) t = kGemvTile;
+    if (t == -1 && splitk)
+      t = nt16                           ? kSplitK32W16
+          : std::min(p.m, p.n) <= 64 ? kSplitK32
+                                         : kSplitK;
     if (t == -1) {
       // Rounds of resident tiles on the 256 CUs: one 256x256 tile (8
       // waves) per CU, two 128x128 tiles per CU. Measured on MI355X, a
@@ -544,7 +566,8 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
   }
   const bool fast = half && (c.tile == kFastTile256 || c.tile == kFastTile192 ||
                              c.tile == kFastTile128);
-  const bool splitk = c.tile == kSplitK || c.tile == kSplitK32;
+  const bool splitk =
+      c.tile == kSplitK || c.tile == kSplitK32 || c.tile == kSplitK32W16;
   const bool x3 = c.tile == kF32x3Tile128 || c.tile == kF32x3Tile64;
   const bool gemv = c.tile == kGemvTile;
   if (gemv) {
@@ -552,8 +575,9 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
              std::to_string(p.m) + "_k" + std::to_string(p.k);
     return c;
   }
-  c.name = std::string(splitk     ? (c.tile == kSplitK ? "gemm_splitk4_"
-                                                       : "gemm_splitk8_")
+  c.name = std::string(splitk     ? (c.tile == kSplitK     ? "gemm_splitk4_"
+                                     : c.tile == kSplitK32 ? "gemm_splitk8_"
+                                                           : "gemm_splitk16_")
                        : x3       ? "gemm_f32x3_"
                        : !half    ? "gemm_mfma_"
                        : fast     ? "gemm_fast_"
@@ -591,6 +615,8 @@ qk_status DispatchHalf(int tile, const GemmArgs& g, int batch, bool ta,
       return DispatchSplitK<T, 64, 4>(g, batch, ta, tb, st, name);
     case kSplitK32:
       return DispatchSplitK<T, 32, 8>(g, batch, ta, tb, st, name);
+    case kSplitK32W16:
+      return DispatchSplitKNT16<T>(g, batch, st, name);
     default:
       return DispatchTile<T, 64, 64, 64, 2, 2>(g, batch, ta, tb, st, name);
   }

@@ -285,9 +285,14 @@ def test_split_k_kernel(dev, ta, tb):
 @pytest.mark.parametrize("ta", [False, True])
 @pytest.mark.parametrize("tb", [False, True])
 def test_split_k_kernel_few_rows(dev, ta, tb):
-    """At most 64 rows (or columns): 32x32 tiles, eight waves over K."""
+    """At most 64 rows (or columns): 32x32 tiles, eight waves over K
+    (sixteen for at most 16 rows against NT weights)."""
     plan = run_case(dev, 16, 700, 2048, ta=ta, tb=tb)
-    assert "gemm_splitk8" in plan.describe()
+    want = "gemm_splitk16" if (not ta and tb) else "gemm_splitk8"
+    assert want in plan.describe()
+    plan = run_case(dev, 11, 130, 1088, ta=ta, tb=tb, tin="float16",
+                    epilogue=Epilogue.kBiasThenGELU, beta=0.5)
+    assert want in plan.describe()
     plan = run_case(dev, 64, 512, 2048, ta=ta, tb=tb)
     assert "gemm_splitk8" in plan.describe()
     plan = run_case(dev, 61, 1030, 1024, ta=ta, tb=tb, tin="float16")
@@ -307,9 +312,11 @@ def test_wide_gemv_few_rows(dev, m, k):
         plan = run_case(dev, m, 77, k, tb=True)
         assert "gemv_nt" not in plan.describe()
         return
+    # 7..16 rows with K >= 1024: the sixteen-wave split-K kernel instead
+    want = "gemm_splitk16" if m > 6 and k >= 1024 else "gemv_nt"
     for n, tin in ((77, "bfloat16"), (1000, "float16"), (6144, "bfloat16")):
         plan = run_case(dev, m, n, k, tb=True, tin=tin, seed=m * k + n)
-        assert "gemv_nt" in plan.describe(), plan.describe()
+        assert want in plan.describe(), plan.describe()
 
 
 def test_wide_gemv_epilogues_batches_and_layouts(dev):
