@@ -215,14 +215,14 @@ def secondary(torch, qkern, dev, gen):
                     "kernel": plan.describe().split("kernel=")[-1]})
         del a, b, d
     if want("int4"):
-        # int4 batched rows (decode batch / prefill), M = 16 and 512 at the
-        # four Qwen3-8B shapes of the int4 config (weights rotated over at
+        # int4 batched rows (decode batch / prefill), M = 4 (the top of the
+        # reference's matvec range), 16 and 512 at the four Qwen3-8B shapes of the int4 config (weights rotated over at
         # least 600 MB)
         for n, k in [(12288, 4096), (4096, 4096), (4096, 12288),
                      (151936, 4096)]:
             nset = min(8, max(2, -(-(600 << 20) // (n * k // 2))))
             sets = [make_int4(torch, dev, n, k, gen) for _ in range(nset)]
-            for m in (16, 512):
+            for m in (4, 16, 512):
                 x = torch.randn(m, k, device=dev, generator=gen).to(
                     torch.bfloat16)
                 y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
@@ -248,7 +248,7 @@ def secondary(torch, qkern, dev, gen):
             b = (0.05 * torch.randn(n, k // GROUP, device=dev, generator=gen)).to(
                 torch.bfloat16)
             sets8.append((codes, s, b))
-        for m in (1, 8, 128):
+        for m in (1, 4, 8, 128):
             x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
             y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
             fn = lambda i: qkern.qmatvec(x, *sets8[i % 12], out=y,

@@ -1457,10 +1457,16 @@ qk_status LaunchQMatvec(const QuantProblem& p, hipStream_t stream) {
   // lm_head, 74 against 118 us at M = 16; 12288 x 4096 11 against 12);
   // with fewer, reading all of x per workgroup costs more than the skinny
   // kernels' single round (8192 x 4096 10 against 8).
-  if (m > 4 && qstream && QStreamApplies(p) &&
+  // From two rows on, the MFMA streaming kernels beat the dot-product
+  // streams (int8 12288 x 4096: M = 2 / 4 21.3 / 30.5 us on the streams,
+  // 14.6 us for M = 5 on the skinny kernel). QK_QMV_MFMA_MIN_M: fewest rows
+  // for them (tuning; read at every call).
+  const char* mmv = std::getenv("QK_QMV_MFMA_MIN_M");
+  const int mfma_min_m = mmv == nullptr ? 2 : std::max(2, std::atoi(mmv));
+  if (m >= mfma_min_m && qstream && QStreamApplies(p) &&
       (qstream_all || QStreamRounds(p, DeviceComputeUnits()) >= 3))
     return LaunchQStream(p, stream);
-  if (m > 4 && QSkinnyApplies(p)) return LaunchQSkinny(p, stream);
+  if (m >= mfma_min_m && QSkinnyApplies(p)) return LaunchQSkinny(p, stream);
   // 33..64 rows: the K-split dequantizing kernel where it applies (int4
   // 12288 x 4096: 21 / 24 us at M = 33 / 64 against 31 for the GEMM).
   const bool mid = m > 4 && QMidApplies(p);

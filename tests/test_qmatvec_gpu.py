@@ -437,6 +437,34 @@ def test_qmatvec_reference_quantizer_end_to_end(dev):
     assert O.rel_fro(y8.float().cpu().numpy(), want8) <= 1e-2
 
 
+@pytest.mark.parametrize("mnk", [(2, 300, 4096), (3, 77, 1024),
+                                 (4, 4100, 2048), (2, 12400, 1024),
+                                 (4, 13000, 4096), (3, 520, 12288)])
+@pytest.mark.parametrize("packing", [Packing.U32X8, Packing.U8,
+                                     Packing.S8_SYM])
+def test_qmatvec_two_to_four_rows_both_paths(dev, mnk, packing, monkeypatch):
+    """2..4 rows of bf16 x (the reference's matvec range, ROWS_MAX = 4,
+    qwen3.py:215-230) with group-64 codes: the MFMA streaming kernels (the
+    skinny kernel; for int4 over wide N with K <= 4096 the streamed kernel)
+    and, with QK_QMV_MFMA_MIN_M=5, the dot-product streams they replace;
+    ragged N, with and without offsets, each against the float64 oracle."""
+    m, n, k = mnk
+    rng = np.random.default_rng(m * 11 + n + int(packing))
+    for has_bias in (True, False):
+        dc, ds, db, w, *_ = make_weights(rng, n, k, packing, 64,
+                                         has_bias=has_bias)
+        x = O.round_to(rng.standard_normal((m, k)), "bfloat16").astype(
+            np.float32)
+        args = (torch.from_numpy(x).to(torch.bfloat16).to(dev), dc.to(dev),
+                ds.to(dev), None if db is None else db.to(dev))
+        for floor in ("2", "5"):
+            monkeypatch.setenv("QK_QMV_MFMA_MIN_M", floor)
+            y = qkern.qmatvec(*args, packing=packing)
+            torch.cuda.synchronize()
+            check_matvec(y.float().cpu().numpy().astype(np.float64), x, w)
+        monkeypatch.delenv("QK_QMV_MFMA_MIN_M")
+
+
 @pytest.mark.parametrize("mnk", [(5, 16400, 512), (16, 12400, 1024),
                                  (9, 20000, 2048), (16, 13000, 4096),
                                  (12, 18990, 4096), (16, 40000, 4096)])
@@ -584,7 +612,7 @@ def config_rows(m):
     return np.r_[0, 192:320, m - 1]
 
 
-@pytest.mark.parametrize("m", [1, 16, 512])
+@pytest.mark.parametrize("m", [1, 4, 16, 512])
 @pytest.mark.parametrize("nk", QWEN3_8B, ids=[f"{n}x{k}" for n, k in QWEN3_8B])
 def test_config_int4(dev, nk, m):
     # every shape at M = 1 (decode), 16 and 512
@@ -602,7 +630,7 @@ def test_config_int4_lm_head_128_rows(dev):
                     seed=4)
 
 
-@pytest.mark.parametrize("m", [1, 8, 128])
+@pytest.mark.parametrize("m", [1, 4, 8, 128])
 def test_config_int8_affine(dev, m):
     n, k = 12288, 4096
     wts = config_weights(dev, n, k, 8)
