@@ -276,7 +276,7 @@ qk_status DispatchTile(const GemmArgs& g, int batch, bool ta, bool tb,
 template <typename T, int BN, int NW = 4, bool MC = false>
 qk_status DispatchFastM(const GemmArgs& g, int batch, bool ta, bool tb,
                         hipStream_t stream, const char* name) {
-  dim3 grid(g.tiles_m * g.tiles_n, batch);
+  dim3 grid(g.tiles_m * g.tiles_n, batch, g.ksplit);
   if (!ta && !tb)
     gemm_dma_kernel<T, BN, false, false, NW, MC><<<grid, NW * 64, 0, stream>>>(g);
   else if (!ta && tb)
@@ -504,6 +504,38 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
         if (r < best) best = r, t = c.tile;
       }
     }
+    // Too few 256 x 128 tiles to occupy the CUs, more than 64 rows and one
+    // batch entry: the same tiles with K split over workgroups (partials
+    // summed in K order by the last workgroup of each tile), the largest
+    // power-of-two split up to 8 that keeps every workgroup resident (one
+    // per CU) with at least 16 K tiles per split; where the split-K 64 x 64
+    // kernel below takes one round of workgroups and K is below 8192 that
+    // kernel instead. Measured on MI355X (bf16, us, split / previous):
+    // 512 x 4096 x 12288 76 / 163, 256 x 4096 x 12288 63 / 78, 256 x 12288
+    // x 4096 46 / 72, 384 x 4096 x 4096 36 / 48; 128 x 4096 x 4096 32 / 26
+    // (the split-K kernel kept). QK_GEMM_KSPLIT=<s> forces the split where
+    // the tiles apply, 0 turns the path off (tuning and tests).
+    const bool splitk =
+        tiles(64, 64) < 2 * cus && CeilDiv(p.k, 64) >= 16;
+    // (A [M][K] against NT weights, at most 128 rows: the split-K kernel
+    // also over two rounds, 128 x 12288 x 4096 41 against 49 us.)
+    const bool nt_layout = !p.a.transpose && p.b.transpose;
+    if (t < 0 && p.batch <= 1 && p.m > 64 && FastApplies(p, 128)) {
+      const char* v = std::getenv("QK_GEMM_KSPLIT");
+      const int forced = v == nullptr ? -1 : std::atoi(v);
+      const int64_t nt = tiles(256, 128), kt = p.k / 64;
+      int split = 1;
+      if (forced > 0) {
+        split = static_cast<int>(std::min<int64_t>(forced, kt));
+      } else if (forced < 0 &&
+                 (p.k >= 8192 || !splitk ||
+                  (tiles(64, 64) > cus &&
+                   !(nt_layout && p.m <= 128)))) {
+        for (int s2 = 2; s2 <= 8; s2 *= 2)
+          if (nt * s2 <= cus && kt / s2 >= 16) split = s2;
+      }
+      if (split > 1) t = kFastTile128, c.split_k = split;
+    }
     // At most eight rows of x against NT weights: the wide gemv
     // (bandwidth-bound on the weights).
     // Few 64x64 tiles and a long K: split K over the waves of each tile
@@ -512,7 +544,6 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
     // 28 x [64, 1024] x [1024, 6144]^T 312 -> 229 us on MI355X). At most 16
     // rows against NT weights: sixteen waves, twice the loads in flight per
     // workgroup (M = 16 184 -> 168 us; M = 8 173 us against the gemv's 200).
-    const bool splitk = tiles(64, 64) < 2 * cus && CeilDiv(p.k, 64) >= 16;
     const bool nt16 = splitk && p.m <= 16 && !p.a.transpose && p.b.transpose;
     if (t < 0 && GemvApplies(p) && !(nt16 && p.m > 6)) t = kGemvTile;
     if (t == -1 && splitk)
@@ -587,7 +618,8 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
            (c.tile >= 0 ? "_w" + std::to_string(kHalfTiles[c.tile].wm *
                                                 kHalfTiles[c.tile].wn)
                         : std::string()) +
-           (p.a.transpose ? "_t" : "_n") + (p.b.transpose ? "t" : "n");
+           (p.a.transpose ? "_t" : "_n") + (p.b.transpose ? "t" : "n") +
+           (c.split_k > 1 ? "_ks" + std::to_string(c.split_k) : std::string());
   return c;
 }
 
@@ -624,7 +656,8 @@ qk_status DispatchHalf(int tile, const GemmArgs& g, int batch, bool ta,
 
 qk_status LaunchGemm(const GemmProblem& p, hipStream_t stream) {
   const GemmKernelChoice c = ChooseGemmKernel(p);
-  GemmArgs g;
+  GemmArgs g{};
+  g.ksplit = 1;
   g.a = p.a.ptr;
   g.b = p.b.ptr;
   g.c = p.c;
@@ -671,6 +704,16 @@ qk_status LaunchGemm(const GemmProblem& p, hipStream_t stream) {
   const int batch = static_cast<int>(p.batch);
   const bool ta = p.a.transpose, tb = p.b.transpose;
   const char* name = c.name.c_str();
+  if (c.split_k > 1) {
+    // f32 partial tiles in the stream's library workspace; without one
+    // (it cannot grow while the stream is captured) one workgroup per tile.
+    const size_t bytes = static_cast<size_t>(g.tiles_m) * g.tiles_n *
+                         c.split_k * c.bm * c.bn * sizeof(float);
+    if (bytes < (size_t{1} << 31) &&
+        static_cast<size_t>(g.tiles_m) * g.tiles_n <= kWsFlagBytes / 4 &&
+        StreamWorkspace(stream, bytes, &g.ws, &g.wsflag))
+      g.ksplit = c.split_k;
+  }
   if (c.tile == kGemvTile) return LaunchGemv(p, stream);
   switch (p.a.dtype) {
     case QK_BF16:

@@ -616,6 +616,110 @@ __device__ __forceinline__ void store_direct(
   else go(T{});
 }
 
+// Store of a tile whose K range may be split over workgroups (K split
+// g.ksplit > 1; batch 0 only): workgroup z of output tile `tile` holds the
+// sum over K range z in acc. It writes that f32 partial tile to the
+// workspace g.ws (slot tile * ksplit + z; values 4 u .. 4 u + 3 of
+// fragment q of thread t at float4 ((slot kPer / 4) + 4 q + u) NT + t, so
+// the stores are coalesced) through a buffer descriptor with the sc1 cache
+// policy (device-coherent: write-through stores, loads that miss stale
+// lines), waits for the stores to complete and then counts itself in on
+// the tile's arrival counter g.wsflag[tile] (a device-scope atomic; the
+// wait, not a device-scope fence, orders "partial, then arrival": a fence
+// would write back and invalidate the whole L2). The last to arrive resets
+// the counter to zero for the next launch, sums the partials in the order
+// z = 0, 1, ... (its own from registers: first when z <= 1, the first
+// addition commuting; for z >= 2 the sum restarts from partial 0 and
+// reloads its own in place), so the result does not depend on the arrival
+// order, and stores the tile with the epilogue. No workgroup waits for
+// another. lds_flag: one word of LDS no wave still reads.
+template <typename T, int BM, int BN, int WM, int WN, bool MC, int NT>
+__device__ __forceinline__ void split_k_store(
+    const GemmArgs& g, f32x16 (&acc)[BM / WM / 32][BN / WN / 32], int tile,
+    int z, int m0, int n0, int tid, int lane, int wm, int wn,
+    uint32_t* lds_flag) {
+  constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
+  const int nc = g.ksplit;
+  if (nc <= 1) {
+    store_direct<T, BM, BN, WM, WN, MC>(g, acc, m0, n0, 0, lane, wm, wn);
+    return;
+  }
+  auto slot = [&](int idx) { return tile * nc + idx; };
+  constexpr int kPer = FM * FN * 16;
+  const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(
+      g.ws, (short)0, 0x7FFFFFFF, 0x00020000);
+  constexpr int kSc1 = 16;
+  auto part_off = [&](int sl, int q, int u) {
+    return (((sl * (kPer / 4)) + q * 4 + u) * NT + tid) * 16;
+  };
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        f32x4 v = {acc[i][j][4 * u], acc[i][j][4 * u + 1],
+                   acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, v), wsr, part_off(slot(z), i * FN + j, u),
+            0, kSc1);
+      }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(
+        g.wsflag + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t last = old + 1 == static_cast<uint32_t>(nc);
+    if (last)
+      __hip_atomic_store(g.wsflag + tile, 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    *lds_flag = last;
+  }
+  __syncthreads();
+  if (*lds_flag == 0) return;
+  // kChunk fragments at a time, all loads of a chunk issued together (one
+  // memory round trip per partial and chunk); two fragments, 32 values: a
+  // larger chunk raised the register count of the kernels into spills.
+  constexpr int kFrags = FM * FN;
+  constexpr int kChunk = kFrags < 2 ? kFrags : 2;
+  const int start = z >= 2 ? 1 : 0;
+#pragma unroll
+  for (int q0 = 0; q0 < kFrags; q0 += kChunk) {
+    auto load_into = [&](int idx, float (&v)[kChunk][16]) {
+      const int sl = slot(idx);
+#pragma unroll
+      for (int q = 0; q < kChunk; ++q)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const f32x4 l = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         wsr, part_off(sl, q0 + q, u), 0, kSc1));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[q][4 * u + e] = l[e];
+        }
+    };
+    float v[kChunk][16];
+    if (z >= 2) {
+      load_into(0, v);
+#pragma unroll
+      for (int q = 0; q < kChunk; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          acc[(q0 + q) / FN][(q0 + q) % FN][r] = v[q][r];
+    }
+    for (int idx = start; idx < nc; ++idx) {
+      if (idx == z && z <= 1) continue;
+      load_into(idx, v);
+#pragma unroll
+      for (int q = 0; q < kChunk; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          acc[(q0 + q) / FN][(q0 + q) % FN][r] += v[q][r];
+    }
+  }
+  store_direct<T, BM, BN, WM, WN, MC>(g, acc, m0, n0, 0, lane, wm, wn);
+}
+
 // MC: M need not be a multiple of BM (A rows past M read zeros through the
 // descriptor's extent, output rows past M are not stored); AK only.
 // DEPTH = 2 keeps two register sets of operand loads in flight, so a

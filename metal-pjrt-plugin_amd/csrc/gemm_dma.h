@@ -37,6 +37,11 @@
 //    wait for the DMA into the other. Their completion is awaited
 //    explicitly before each barrier and before the kernel ends.
 //  - The epilogue is applied from the accumulators (store_direct).
+//  - K split over workgroups (g.ksplit > 1, one batch entry, for grids
+//    whose tiles alone would leave CUs idle): workgroup (tile, z =
+//    blockIdx.z) takes K tiles z T / ksplit .. (z + 1) T / ksplit and the
+//    partial tiles meet in split_k_store (summed in K order by the last
+//    to arrive).
 #pragma once
 
 #include "gemm_common.h"
@@ -219,6 +224,10 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(GemmArgs g) {
   const int tn = (bid % group_span) / gsz;
   const int m0 = tm * BM, n0 = tn * BN;
   const long long batch = blockIdx.y;
+  const int ktiles = g.k / BK;  // >= 1
+  const int z = blockIdx.z;
+  const int kbeg = z * ktiles / g.ksplit;
+  const int kend = (z + 1) * ktiles / g.ksplit;  // > kbeg: ksplit <= ktiles
 
   LA la;
   LB lb;
@@ -250,9 +259,8 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int ktiles = g.k / BK;  // >= 1
-  issue_all(st0, 0);
-  issue_all(st1, min(1, ktiles - 1) * BK);
+  issue_all(st0, kbeg * BK);
+  issue_all(st1, min(kbeg + 1, kend - 1) * BK);
   __builtin_amdgcn_s_waitcnt(VmcntImm(kDma));  // tile 0 has landed
   __syncthreads();
 #pragma unroll
@@ -286,7 +294,7 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(GemmArgs g) {
     // after the barrier nobody reads cs: step 3 runs from registers.
     __builtin_amdgcn_s_waitcnt(VmcntImm(0));
     __syncthreads();
-    const int k2 = min(kt + 2, ktiles - 1) * BK;
+    const int k2 = min(kt + 2, kend - 1) * BK;
     // Step 3: each MFMA is followed by kDmaPer DMAs of tile kt + 2 into cs
     // and one fragment read of the next tile's first K step from ns, pinned in
     // that order by scheduling barriers.
@@ -308,15 +316,22 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(GemmArgs g) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  int kt = 0;
-  for (; kt + 1 < ktiles; kt += 2) {
+  int kt = kbeg;
+  for (; kt + 1 < kend; kt += 2) {
     tile(st0, st1, kt);
     tile(st1, st0, kt + 1);
   }
-  if (kt < ktiles) tile(st0, st1, kt);
+  if (kt < kend) tile(st0, st1, kt);
   // No DMA may still be writing this workgroup's LDS when it ends.
   __builtin_amdgcn_s_waitcnt(VmcntImm(0));
-  store_direct<T, BM, BN, WM, WN, MC>(g, acc, m0, n0, batch, lane, wm, wn);
+  if (g.ksplit > 1) {
+    __syncthreads();  // every wave is done with st0 (the arrival word)
+    split_k_store<T, BM, BN, WM, WN, MC, NWV * 64>(
+        g, acc, blockIdx.x, z, m0, n0, tid, lane, wm, wn,
+        reinterpret_cast<uint32_t*>(st0));
+  } else {
+    store_direct<T, BM, BN, WM, WN, MC>(g, acc, m0, n0, batch, lane, wm, wn);
+  }
 }
 
 }  // namespace

@@ -410,102 +410,9 @@ qgemm_dma_kernel(GemmArgs g) {
   QTilesTail<0, S - 1>(tile_step, kt, kend);
   // No DMA may still be writing this workgroup's LDS when it ends.
   __builtin_amdgcn_s_waitcnt(VmcntImm(0));
-  if (splits == 1) {
-    store_direct<T, BM, BN, WM, WN, MC>(g, acc, m0, n0, 0, lane, wm, wn);
-  } else {
-    // K range z of the tile: contributors z = 0 .. splits - 1 (K order),
-    // partial slot tile splits + z.
-    const int nc = splits, me = z;
-    auto slot = [&](int idx) { return tile * splits + idx; };
-    // Partial tiles through a buffer descriptor with the sc1 cache policy
-    // (device-coherent: write-through stores, loads that miss stale
-    // lines), 16 bytes per lane: values 4 u .. 4 u + 3 of fragment
-    // q = i FN + j of thread t at float4 ((slot kPer / 4) + q 4 + u) NT + t
-    // (coalesced). The order "partial, then arrival" comes from waiting
-    // for the stores to complete before the device-scope counter is
-    // incremented; a device-scope fence would do the same by writing back
-    // and invalidating the whole L2, which costs the other workgroups
-    // their cached x and codes.
-    constexpr int kPer = FM * FN * 16;
-    const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(
-        g.ws, (short)0, 0x7FFFFFFF, 0x00020000);
-    constexpr int kSc1 = 16;
-    auto part_off = [&](int sl, int q, int u) {
-      return (((sl * (kPer / 4)) + q * 4 + u) * C::NT + tid) * 16;
-    };
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          f32x4 v = {acc[i][j][4 * u], acc[i][j][4 * u + 1],
-                     acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]};
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(u32x4, v), wsr, part_off(slot(me), i * FN + j, u),
-              0, kSc1);
-        }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    uint32_t* const flag = reinterpret_cast<uint32_t*>(smem);
-    if (tid == 0) {
-      const uint32_t old = __hip_atomic_fetch_add(
-          g.wsflag + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const uint32_t last = old + 1 == static_cast<uint32_t>(nc);
-      if (last)
-        __hip_atomic_store(g.wsflag + tile, 0u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      *flag = last;
-    }
-    __syncthreads();
-    if (*flag != 0) {
-      // The sum in K order, ((p0 + p1) + p2) + ..., in place: the own
-      // partial stands first when me <= 1 (the first addition commutes);
-      // for me >= 2 the sum restarts from p0 and reloads the own partial
-      // in its place. kChunk fragments at a time, all loads of a chunk
-      // issued together (one memory round trip per partial and chunk).
-      constexpr int kFrags = FM * FN;
-      // (Two fragments, 32 values: a larger chunk raised the register
-      // count of the whole kernel into spills.)
-      constexpr int kChunk = kFrags < 2 ? kFrags : 2;
-      const int start = me >= 2 ? 1 : 0;
-#pragma unroll
-      for (int q0 = 0; q0 < kFrags; q0 += kChunk) {
-        auto load_into = [&](int idx, float (&v)[kChunk][16]) {
-          const int sl = slot(idx);
-#pragma unroll
-          for (int q = 0; q < kChunk; ++q)
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const f32x4 l = __builtin_bit_cast(
-                  f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                             wsr, part_off(sl, q0 + q, u), 0, kSc1));
-#pragma unroll
-              for (int e = 0; e < 4; ++e) v[q][4 * u + e] = l[e];
-            }
-        };
-        float v[kChunk][16];
-        if (me >= 2) {
-          load_into(0, v);
-#pragma unroll
-          for (int q = 0; q < kChunk; ++q)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-              acc[(q0 + q) / FN][(q0 + q) % FN][r] = v[q][r];
-        }
-        for (int idx = start; idx < nc; ++idx) {
-          if (idx == me && me <= 1) continue;
-          load_into(idx, v);
-#pragma unroll
-          for (int q = 0; q < kChunk; ++q)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-              acc[(q0 + q) / FN][(q0 + q) % FN][r] += v[q][r];
-        }
-      }
-      store_direct<T, BM, BN, WM, WN, MC>(g, acc, m0, n0, 0, lane, wm, wn);
-    }
-  }
+  split_k_store<T, BM, BN, WM, WN, MC, C::NT>(
+      g, acc, tile, z, m0, n0, tid, lane, wm, wn,
+      reinterpret_cast<uint32_t*>(smem));
 }
 
 

@@ -275,7 +275,7 @@ def test_activation_special_values(dev, epilogue):
 def test_split_k_kernel(dev, ta, tb):
     """Few output tiles and a long K run the split-K kernel (each wave a
     quarter of K, reduced through LDS): ragged M/N/K, all transposes."""
-    plan = run_case(dev, 80, 512, 2048, ta=ta, tb=tb)
+    plan = run_case(dev, 80, 520, 2048, ta=ta, tb=tb)
     assert "gemm_splitk4" in plan.describe()
     plan = run_case(dev, 100, 260, 1500, ta=ta, tb=tb, tin="float16",
                     beta=0.5)
@@ -300,6 +300,87 @@ def test_split_k_kernel_few_rows(dev, ta, tb):
     plan = run_case(dev, 300, 5, 1100, ta=ta, tb=tb, tin="float16",
                     epilogue=Epilogue.kBiasThenSILU)
     assert "gemm_splitk8" in plan.describe()
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_fast_tiles_k_split(dev, ta, tb):
+    """Few 256 x 128 tiles and more than 64 rows: the LDS-DMA tile kernel
+    with K split over workgroups, partials summed in K order by the last
+    workgroup of each tile (ragged M, every epilogue term, f32 output)."""
+    plan = run_case(dev, 200, 1024, 8192, ta=ta, tb=tb)
+    assert "gemm_fast" in plan.describe() and "_ks8" in plan.describe()
+    plan = run_case(dev, 296, 512, 8192, ta=ta, tb=tb, tin="float16",
+                    epilogue=Epilogue.kBiasThenSILUWithAux, separate_c=True,
+                    beta=0.5, alpha=1.5, pad=8)
+    assert "_ks8" in plan.describe()
+    plan = run_case(dev, 72, 128, 8192, ta=ta, tb=tb, tout="float32",
+                    epilogue=Epilogue.kBiasThenGELU)
+    assert "_ks8" in plan.describe()
+    # 64 x 64 split-K workgroups beyond one round: 384 x 4096 x 4096
+    plan = run_case(dev, 384, 4096, 4096, ta=ta, tb=tb)
+    assert "_ks4" in plan.describe()
+
+
+def test_fast_tiles_k_split_forced_and_repeated(dev, monkeypatch):
+    # uneven K ranges (32 K tiles in 3 and 5 parts), one K tile per part,
+    # and the arrival counters reset for the next launch: the same plan
+    # executed twice in a row on the same stream
+    for split, k in (("3", 2048), ("5", 2048), ("16", 1024)):
+        monkeypatch.setenv("QK_GEMM_KSPLIT", split)
+        plan = run_case(dev, 130, 256, k, tb=True, seed=int(split))
+        assert f"_ks{split}" in plan.describe()
+        plan = run_case(dev, 130, 256, k, tb=True, seed=int(split))
+    monkeypatch.setenv("QK_GEMM_KSPLIT", "0")
+    plan = run_case(dev, 200, 1024, 2048)
+    assert "_ks" not in plan.describe()
+    monkeypatch.delenv("QK_GEMM_KSPLIT")
+
+
+def test_fast_tiles_k_split_graph_replay(dev):
+    # captured into a HIP graph after an eager call on the capturing stream
+    # (its workspace exists), replayed three times with an eager K-split
+    # GEMM of another shape on that stream between the replays, each replay
+    # against the eager result
+    from qkern import blas as L
+
+    def setup(m, n, k, seed):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        x = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
+        w = torch.randn(k, n, device=dev, generator=g).to(torch.bfloat16)
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        plan = L.BlasLt.get_matmul_plan(
+            L.GemmConfig(L.MatrixLayout("bfloat16", m, k),
+                         L.MatrixLayout("bfloat16", k, n),
+                         L.MatrixLayout("bfloat16", m, n),
+                         L.MatrixLayout("bfloat16", m, n)),
+            L.Epilogue.kDefault)
+        return plan, L.MemoryArgs(x, w, None, y), x, w, y
+
+    plan, args, x, w, y = setup(200, 1024, 8192, 5)
+    plan2, args2, *_ = setup(296, 512, 8192, 6)
+    assert "_ks8" in plan.describe() and "_ks8" in plan2.describe()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        plan.execute_on_stream(s, args)
+    torch.cuda.synchronize()
+    want = y.clone()
+    ref = x.float() @ w.float()
+    assert ((want.float() - ref).abs() <= 2e-2 * ref.abs() + 2e-2).all()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            plan.execute_on_stream(s, args)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        y.fill_(7.0)
+        with torch.cuda.stream(s):
+            plan2.execute_on_stream(s, args2)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want)
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
