@@ -520,7 +520,12 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
     // (A [M][K] against NT weights, at most 128 rows: the split-K kernel
     // also over two rounds, 128 x 12288 x 4096 41 against 49 us.)
     const bool nt_layout = !p.a.transpose && p.b.transpose;
-    if (t < 0 && p.batch <= 1 && p.m > 64 && FastApplies(p, 128)) {
+    // (Also 256 x 128 tiles that leave half the CUs idle at K >= 8192:
+    // 1024 x 4096 x 12288 split 2.)
+    const bool few128 = t == kFastTile128 && p.k >= 8192 &&
+                        ForcedHalfTile() < 0;
+    if ((t < 0 || few128) && p.batch <= 1 && p.m > 64 &&
+        FastApplies(p, 128)) {
       const char* v = std::getenv("QK_GEMM_KSPLIT");
       const int forced = v == nullptr ? -1 : std::atoi(v);
       const int64_t nt = tiles(256, 128), kt = p.k / 64;

@@ -337,6 +337,30 @@ def test_fast_tiles_k_split_forced_and_repeated(dev, monkeypatch):
     monkeypatch.delenv("QK_GEMM_KSPLIT")
 
 
+def test_fast_tiles_k_split_half_filled(dev):
+    # 1024 x 4096 x 12288: 128 tiles of 256 x 128 would leave half the CUs
+    # idle, so K is split in two; checked against a float32 torch matmul
+    from qkern import blas as L
+    m, n, k = 1024, 4096, 12288
+    g = torch.Generator(device=dev).manual_seed(9)
+    x = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(k, n, device=dev, generator=g) / 64).to(torch.bfloat16)
+    bias = torch.randn(n, device=dev, generator=g).to(torch.bfloat16)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    plan = L.BlasLt.get_matmul_plan(
+        L.GemmConfig(L.MatrixLayout("bfloat16", m, k),
+                     L.MatrixLayout("bfloat16", k, n),
+                     L.MatrixLayout("bfloat16", m, n),
+                     L.MatrixLayout("bfloat16", m, n)), L.Epilogue.kBias)
+    assert "_ks2" in plan.describe()
+    plan.execute_on_stream(None, L.MemoryArgs(x, w, None, y, bias))
+    torch.cuda.synchronize()
+    ref = x.float() @ w.float() + bias.float()
+    err = (y.float() - ref).abs()
+    # one bf16 rounding of the output over an f32 sum
+    assert (err <= 2 ** -8 * ref.abs() + 1e-3 * ref.abs().max()).all()
+
+
 def test_fast_tiles_k_split_graph_replay(dev):
     # captured into a HIP graph after an eager call on the capturing stream
     # (its workspace exists), replayed three times with an eager K-split
