@@ -9,8 +9,10 @@ copies of the weight set (1.25 GB) are rotated so that no launch reads
 weights another launch left in the 256 MB Infinity Cache.
 
 Also reported (`secondary`): bf16 GEMM + bias + SiLU TFLOP/s at the C3
-shapes (the metric's second half, beside hipBLASLt), f32 GEMM 1024^3,
-int4 M = 16 / 512 at the four Qwen3-8B shapes, int8 affine M = 1 / 8 / 128,
+shapes (the metric's second half, beside hipBLASLt), bf16 GEMM at
+prefill row counts whose tiles alone would not fill the CUs (beside
+hipBLASLt), f32 GEMM 1024^3, int4 M = 4 / 16 / 512 at the four Qwen3-8B
+shapes, int8 affine M = 1 / 4 / 8 / 128,
 RMSNorm, softmax and LayerNorm [4096, 4096], the reference's few-row GEMM
 list, decode attention, the int4 embedding gather, device quantization of
 a projection and device copies (the read + write ceiling); each against
@@ -188,6 +190,34 @@ def secondary(torch, qkern, dev, gen):
                 lambda: torch.matmul(a, b, out=d))
             tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
             out.append({"name": f"bf16 gemm+bias+silu {m}x{n}x{k}",
+                        "value": round(tf, 1), "unit": "TFLOP/s",
+                        "ms": round(ms, 4), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                        "kernel": plan.describe().split("kernel=")[-1],
+                        "hipblaslt_matmul_tflops": round(
+                            2.0 * m * n * k / (ms_lt * 1e-3) / 1e12, 1)})
+            del a, b, d
+    if want("gemm_mid"):
+        # bf16 GEMM D = A @ B (NN, no epilogue) at prefill row counts whose
+        # 256 x 128 tiles do not fill the CUs (K split over workgroups), with
+        # hipBLASLt on the same operands timed alternately
+        for (m, n, k) in [(256, 12288, 4096), (512, 4096, 12288),
+                          (1024, 4096, 12288), (384, 4096, 4096)]:
+            a = (torch.randn(m, k, device=dev, generator=gen) / k ** 0.5).to(
+                torch.bfloat16)
+            b = (torch.randn(k, n, device=dev, generator=gen) / k ** 0.5).to(
+                torch.bfloat16)
+            d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            L = qkern.blas
+            lay = lambda r, c: L.MatrixLayout("bfloat16", r, c)
+            plan = L.BlasLt.get_matmul_plan(
+                L.GemmConfig(lay(m, k), lay(k, n), lay(m, n), lay(m, n)),
+                L.Epilogue.kDefault)
+            args = L.MemoryArgs(a, b, None, d)
+            ms, ms_lt = gemm_vs_library(
+                torch, lambda i: plan.execute_on_stream(None, args),
+                lambda: torch.matmul(a, b, out=d))
+            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            out.append({"name": f"bf16 gemm {m}x{n}x{k}",
                         "value": round(tf, 1), "unit": "TFLOP/s",
                         "ms": round(ms, 4), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                         "kernel": plan.describe().split("kernel=")[-1],
@@ -530,7 +560,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None,
                     help="run only these secondary parts (comma list of "
-                         "gemm, f32, int4, int8, rownorm, fewrow, attention, "
+                         "gemm, gemm_mid, f32, int4, int8, rownorm, fewrow, attention, "
                          "embed, copy) and print them, without the headline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 plain device copies of 512 MiB (the "
