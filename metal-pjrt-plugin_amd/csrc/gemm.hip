@@ -550,7 +550,17 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
     // rows against NT weights: sixteen waves, twice the loads in flight per
     // workgroup (M = 16 184 -> 168 us; M = 8 173 us against the gemv's 200).
     const bool nt16 = splitk && p.m <= 16 && !p.a.transpose && p.b.transpose;
-    if (t < 0 && GemvApplies(p) && !(nt16 && p.m > 6)) t = kGemvTile;
+    // At most eight rows of x against NN weights with K >= 8192: the NN
+    // gemv (one workgroup per 32 columns walking all of K; 4096 x 12288
+    // M = 1..4 55 us against 67 on the split-K kernel; at K = 4096 it is
+    // level or slower, 64-byte row pieces). QK_GEMV_NN=0 turns it off,
+    // =2 takes it wherever it applies (tuning and tests, read at every
+    // plan).
+    const char* gnv = std::getenv("QK_GEMV_NN");
+    const bool gemv_nn =
+        (gnv == nullptr ? p.k >= 8192 : *gnv == '2') && GemvNNApplies(p);
+    if (t < 0 && (GemvApplies(p) || gemv_nn) && !(nt16 && p.m > 6))
+      t = kGemvTile;
     if (t == -1 && splitk)
       t = nt16                           ? kSplitK32W16
           : std::min(p.m, p.n) <= 64 ? kSplitK32
@@ -607,7 +617,8 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
   const bool x3 = c.tile == kF32x3Tile128 || c.tile == kF32x3Tile64;
   const bool gemv = c.tile == kGemvTile;
   if (gemv) {
-    c.name = std::string("gemv_nt_") + DTypeName(p.a.dtype) + "_m" +
+    c.name = std::string(p.b.transpose ? "gemv_nt_" : "gemv_nn_") +
+             DTypeName(p.a.dtype) + "_m" +
              std::to_string(p.m) + "_k" + std::to_string(p.k);
     return c;
   }

@@ -51,6 +51,27 @@ __device__ __forceinline__ float Dot8(const u32x4& w, const u32x4& x,
   return acc;
 }
 
+// The BlasLt epilogue of one output (m, n) of batch entry `batch`, in f32
+// with one rounding: v = alpha acc (+ beta C) (+ bias[n]); aux = v;
+// D = act(v).
+template <typename T>
+__device__ __forceinline__ void GemvStore(const GemmArgs& g, long long batch,
+                                          int m, int n, float v) {
+  const long long idx = batch * g.bsd + static_cast<long long>(m) * g.ldd + n;
+  v *= g.alpha;
+  if (g.out_f32) {
+    if (g.use_c) v += g.beta * static_cast<const float*>(g.c)[idx];
+    if (g.has_bias) v += static_cast<const float*>(g.bias)[n];
+    if (g.has_aux) static_cast<float*>(g.aux)[idx] = v;
+    static_cast<float*>(g.d)[idx] = act_f32(g.act, v);
+  } else {
+    if (g.use_c) v += g.beta * to_f32(static_cast<const T*>(g.c)[idx]);
+    if (g.has_bias) v += to_f32(static_cast<const T*>(g.bias)[n]);
+    if (g.has_aux) static_cast<T*>(g.aux)[idx] = from_f32<T>(v);
+    static_cast<T*>(g.d)[idx] = from_f32<T>(act_f32(g.act, v));
+  }
+}
+
 // M rows of x (M <= 8), CPL = K / 512 chunks of 16 bytes per lane and row.
 template <typename T, int M, int CPL>
 __global__ __launch_bounds__(kGemvThreads) void gemv_nt_kernel(GemmArgs g) {
@@ -95,23 +116,6 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_nt_kernel(GemmArgs g) {
                                                         ro, 2);
     }
   };
-  using O = T;
-  auto store = [&](int m, int n, float v) {
-    const long long idx = batch * g.bsd + static_cast<long long>(m) * g.ldd + n;
-    v *= g.alpha;
-    if (g.out_f32) {
-      if (g.use_c) v += g.beta * static_cast<const float*>(g.c)[idx];
-      if (g.has_bias) v += static_cast<const float*>(g.bias)[n];
-      if (g.has_aux) static_cast<float*>(g.aux)[idx] = v;
-      static_cast<float*>(g.d)[idx] = act_f32(g.act, v);
-    } else {
-      if (g.use_c) v += g.beta * to_f32(static_cast<const O*>(g.c)[idx]);
-      if (g.has_bias) v += to_f32(static_cast<const O*>(g.bias)[n]);
-      if (g.has_aux) static_cast<O*>(g.aux)[idx] = from_f32<O>(v);
-      static_cast<O*>(g.d)[idx] = from_f32<O>(act_f32(g.act, v));
-    }
-  };
-
   u32x4 w[D][CPL];
   int n0 = gw;
   if (n0 < g.n) load(n0, w);
@@ -136,8 +140,122 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_nt_kernel(GemmArgs g) {
       const int vi = q + (lane & 3);
       const int d = vi / M, m = vi % M;
       const int n = n0 + d * GW;
-      if (lane < 4 && vi < NV && n < g.n) store(m, n, v);
+      if (lane < 4 && vi < NV && n < g.n) GemvStore<T>(g, batch, m, n, v);
     }
+  }
+}
+
+// NN layout (W stored [K][N], N contiguous), M <= 8 rows of x, K a
+// multiple of 512: one workgroup of eight waves per 32 output columns
+// walks all of K. Lane l holds columns 8 (l % 4) .. + 7 of the
+// workgroup's 32 and K rows 4 (l / 4) .. + 3 of its wave's 64-row window
+// (the window of wave w in step i: rows 512 i + 64 w ..): per step a lane
+// loads four 16-byte pieces of W (each wave-wide load: 16 rows x 64
+// contiguous bytes) and, per row of x, the four matching x values (8
+// bytes), and accumulates M x 8 column sums in f32 (W and x converted
+// exactly, products by FMA). The next step's loads are in flight while
+// one step is computed. The sixteen row groups of a wave are summed by
+// lane shuffles, the eight waves through LDS, and the epilogue is applied
+// per output as in the NT gemv.
+template <typename T, int M>
+__global__ __launch_bounds__(512) void gemv_nn_kernel(GemmArgs g) {
+  __shared__ float part[8][M][32];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 3, r = lane >> 2;
+  const int n0 = blockIdx.x * 32;
+  const long long batch = blockIdx.y;
+  const T* A = static_cast<const T*>(g.a) + batch * g.bsa;
+  const T* B = static_cast<const T*>(g.b) + batch * g.bsb;
+  // W of one batch entry as a buffer (extent: up to the last row's N
+  // values, so columns past N read zeros without a branch).
+  const long long wbytes = (static_cast<long long>(g.k - 1) * g.ldb + g.n) *
+                           static_cast<long long>(sizeof(T));
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<T*>(B), (short)0,
+      static_cast<int>(std::min<long long>(wbytes, 0x7FFFFFFFll)), 0x00020000);
+  // Columns past N (the last workgroup's tail, whole 16-byte pieces as N
+  // is a multiple of 8) read the next row's values, or zeros past the
+  // extent; their sums are not stored.
+  const int coff = (n0 + 8 * c) * static_cast<int>(sizeof(T));
+  const int rstride = g.ldb * static_cast<int>(sizeof(T));
+  const int steps = g.k / 512;
+
+  u32x4 w[2][4];
+  uint32_t xv[2][M][2];
+  auto load = [&](int i, int b) {
+    const int k0 = 512 * i + 64 * wave + 4 * r;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      w[b][u] = __builtin_amdgcn_raw_buffer_load_b128(
+          wrs, coff + (k0 + u) * rstride, 0, 2);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint2 v = *reinterpret_cast<const uint2*>(
+          A + static_cast<long long>(m) * g.lda + k0);
+      xv[b][m][0] = v.x, xv[b][m][1] = v.y;
+    }
+  };
+  float acc[M][8];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[m][e] = 0.f;
+  auto lo16 = [](uint32_t v) { return to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(v & 0xFFFFu))); };
+  auto hi16 = [](uint32_t v) { return to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(v >> 16))); };
+  auto compute = [&](int b) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float wf[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        wf[2 * e] = lo16(w[b][u][e]);
+        wf[2 * e + 1] = hi16(w[b][u][e]);
+      }
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const uint32_t xp = xv[b][m][u >> 1];
+        const float xs = (u & 1) ? hi16(xp) : lo16(xp);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[m][e] = fmaf(xs, wf[e], acc[m][e]);
+      }
+    }
+  };
+  load(0, 0);
+  for (int i = 0; i < steps; i += 2) {
+    if (i + 1 < steps) load(i + 1, 1);
+    compute(0);
+    if (i + 1 >= steps) break;
+    if (i + 2 < steps) load(i + 2, 0);
+    compute(1);
+  }
+  // Sum over the 16 row groups of the wave (lane bits 2..5).
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = acc[m][e];
+      v += __shfl_xor(v, 4);
+      v += __shfl_xor(v, 8);
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      acc[m][e] = v;
+    }
+  if (r == 0) {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[wave][m][8 * c + e] = acc[m][e];
+  }
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < 32 * M) {
+    const int m = t / 32, j = t % 32;
+    float v = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v += part[q][m][j];
+    const int n = n0 + j;
+    if (n < g.n) GemvStore<T>(g, batch, m, n, v);
   }
 }
 
@@ -193,6 +311,25 @@ bool GemvApplies(const GemmProblem& p) {
          p.n <= (int64_t{1} << 30);
 }
 
+bool GemvNNApplies(const GemmProblem& p) {
+  if (p.a.dtype != QK_BF16 && p.a.dtype != QK_F16) return false;
+  if (p.m < 1 || p.m > 8 || p.a.transpose || p.b.transpose) return false;
+  if (p.k % 512 != 0 || p.k == 0 || p.n % 8 != 0 || p.n == 0) return false;
+  const bool batched = p.batch > 1;
+  // x: 8-byte runs of four values; W: 16-byte runs of eight.
+  const int64_t bsa = batched ? p.a.batch_stride : 0;
+  const int64_t bsb = batched ? p.b.batch_stride : 0;
+  if (reinterpret_cast<uintptr_t>(p.a.ptr) % 8 != 0 || p.a.ld % 4 != 0 ||
+      bsa % 4 != 0)
+    return false;
+  if (reinterpret_cast<uintptr_t>(p.b.ptr) % 16 != 0 || p.b.ld % 8 != 0 ||
+      bsb % 8 != 0)
+    return false;
+  // W of one batch entry addressed by a 32-bit buffer offset.
+  return ((p.k - 1) * p.b.ld + p.n + 32) * 2 < (int64_t{1} << 31) &&
+         p.n <= (int64_t{1} << 30);
+}
+
 qk_status LaunchGemv(const GemmProblem& p, hipStream_t stream) {
   GemmArgs g{};
   g.a = p.a.ptr;
@@ -219,6 +356,27 @@ qk_status LaunchGemv(const GemmProblem& p, hipStream_t stream) {
   g.act = p.act;
   g.out_f32 = p.d.dtype == QK_F32;
   const int batch = static_cast<int>(p.batch);
+  if (!p.b.transpose) {
+    const dim3 gr(static_cast<unsigned>((g.n + 31) / 32), batch);
+    auto go = [&](auto tag) {
+      using T = decltype(tag);
+      switch (g.m) {
+        case 1: gemv_nn_kernel<T, 1><<<gr, 512, 0, stream>>>(g); break;
+        case 2: gemv_nn_kernel<T, 2><<<gr, 512, 0, stream>>>(g); break;
+        case 3: gemv_nn_kernel<T, 3><<<gr, 512, 0, stream>>>(g); break;
+        case 4: gemv_nn_kernel<T, 4><<<gr, 512, 0, stream>>>(g); break;
+        case 5: gemv_nn_kernel<T, 5><<<gr, 512, 0, stream>>>(g); break;
+        case 6: gemv_nn_kernel<T, 6><<<gr, 512, 0, stream>>>(g); break;
+        case 7: gemv_nn_kernel<T, 7><<<gr, 512, 0, stream>>>(g); break;
+        default: gemv_nn_kernel<T, 8><<<gr, 512, 0, stream>>>(g); break;
+      }
+    };
+    if (p.a.dtype == QK_BF16)
+      go(bf16{});
+    else
+      go(f16{});
+    return PostLaunch("gemv_nn");
+  }
   const int cpl = g.k / 512;
   // Rounds of kGemvRows rows per wave; at most 8 waves per SIMD of them.
   const int cus = DeviceComputeUnits();
