@@ -550,15 +550,16 @@ GemmKernelChoice ChooseGemmKernel(const GemmProblem& p) {
     // rows against NT weights: sixteen waves, twice the loads in flight per
     // workgroup (M = 16 184 -> 168 us; M = 8 173 us against the gemv's 200).
     const bool nt16 = splitk && p.m <= 16 && !p.a.transpose && p.b.transpose;
-    // At most eight rows of x against NN weights with K >= 8192: the NN
-    // gemv (one workgroup per 32 columns walking all of K; 4096 x 12288
-    // M = 1..4 55 us against 67 on the split-K kernel; at K = 4096 it is
-    // level or slower, 64-byte row pieces). QK_GEMV_NN=0 turns it off,
-    // =2 takes it wherever it applies (tuning and tests, read at every
-    // plan).
+    // At most four rows of x against NN weights of at least 2^25 values:
+    // the NN gemv (one workgroup per 64 columns walking all of K; M = 1
+    // 12288 x 4096 23 us, 4096 x 12288 52, against 47 / 68 on the split-K
+    // kernel and 26 / 62 for hipBLASLt; at 4096 x 4096 and below level or
+    // slower). QK_GEMV_NN=0 turns it off, =2 takes it wherever it applies
+    // (tuning and tests, read at every plan).
     const char* gnv = std::getenv("QK_GEMV_NN");
-    const bool gemv_nn =
-        (gnv == nullptr ? p.k >= 8192 : *gnv == '2') && GemvNNApplies(p);
+    const bool gemv_nn = (gnv == nullptr ? p.n * p.k >= (int64_t{1} << 25)
+                                         : *gnv == '2') &&
+                         GemvNNApplies(p);
     if (t < 0 && (GemvApplies(p) || gemv_nn) && !(nt16 && p.m > 6))
       t = kGemvTile;
     if (t == -1 && splitk)

@@ -19,6 +19,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 #include <string>
 
 #include "gemm_common.h"
@@ -145,25 +146,32 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_nt_kernel(GemmArgs g) {
   }
 }
 
-// NN layout (W stored [K][N], N contiguous), M <= 8 rows of x, K a
-// multiple of 512: one workgroup of eight waves per 32 output columns
-// walks all of K. Lane l holds columns 8 (l % 4) .. + 7 of the
-// workgroup's 32 and K rows 4 (l / 4) .. + 3 of its wave's 64-row window
-// (the window of wave w in step i: rows 512 i + 64 w ..): per step a lane
-// loads four 16-byte pieces of W (each wave-wide load: 16 rows x 64
+// NN layout (W stored [K][N], N contiguous), M <= 4 rows of x, K a
+// multiple of 512: one workgroup of sixteen waves per 64 output columns
+// walks all of K. Lane l holds columns 8 (l % 8) .. + 7 of the
+// workgroup's 64 and K rows 4 (l / 8) .. + 3 of its wave's 32-row window
+// (the window of wave w in step i: rows 512 i + 32 w ..): per step a lane
+// loads four 16-byte pieces of W (each wave-wide load: 8 rows x 128
 // contiguous bytes) and, per row of x, the four matching x values (8
 // bytes), and accumulates M x 8 column sums in f32 (W and x converted
-// exactly, products by FMA). The next step's loads are in flight while
+// exactly, products by FMA; more rows of x exceed the registers of a
+// 1024-thread workgroup). The next step's loads are in flight while
 // one step is computed. The sixteen row groups of a wave are summed by
 // lane shuffles, the eight waves through LDS, and the epilogue is applied
 // per output as in the NT gemv.
-template <typename T, int M>
-__global__ __launch_bounds__(512) void gemv_nn_kernel(GemmArgs g) {
-  __shared__ float part[8][M][32];
+// LPR lanes per W row piece (8: 128 bytes, 64 columns per workgroup; 4
+// lanes, 64-byte pieces, measured at half the bandwidth), NW waves per
+// workgroup; a step covers NW * 256 / LPR rows (512 as used).
+template <typename T, int M, int LPR = 8, int NW = 16>
+__global__ __launch_bounds__(NW * 64) void gemv_nn_kernel(GemmArgs g) {
+  constexpr int CW = 8 * LPR;         // columns per workgroup
+  constexpr int RW = 4 * (64 / LPR);  // rows per wave per step
+  constexpr int RS = NW * RW;         // rows per step
+  __shared__ float part[NW][M][CW];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int c = lane & 3, r = lane >> 2;
-  const int n0 = blockIdx.x * 32;
+  const int c = lane % LPR, r = lane / LPR;
+  const int n0 = blockIdx.x * CW;
   const long long batch = blockIdx.y;
   const T* A = static_cast<const T*>(g.a) + batch * g.bsa;
   const T* B = static_cast<const T*>(g.b) + batch * g.bsb;
@@ -179,12 +187,12 @@ __global__ __launch_bounds__(512) void gemv_nn_kernel(GemmArgs g) {
   // extent; their sums are not stored.
   const int coff = (n0 + 8 * c) * static_cast<int>(sizeof(T));
   const int rstride = g.ldb * static_cast<int>(sizeof(T));
-  const int steps = g.k / 512;
+  const int steps = g.k / RS;
 
   u32x4 w[2][4];
   uint32_t xv[2][M][2];
   auto load = [&](int i, int b) {
-    const int k0 = 512 * i + 64 * wave + 4 * r;
+    const int k0 = RS * i + RW * wave + 4 * r;
 #pragma unroll
     for (int u = 0; u < 4; ++u)
       w[b][u] = __builtin_amdgcn_raw_buffer_load_b128(
@@ -235,10 +243,8 @@ __global__ __launch_bounds__(512) void gemv_nn_kernel(GemmArgs g) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float v = acc[m][e];
-      v += __shfl_xor(v, 4);
-      v += __shfl_xor(v, 8);
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
+#pragma unroll
+      for (int o = LPR; o < 64; o <<= 1) v += __shfl_xor(v, o);
       acc[m][e] = v;
     }
   if (r == 0) {
@@ -249,11 +255,11 @@ __global__ __launch_bounds__(512) void gemv_nn_kernel(GemmArgs g) {
   }
   __syncthreads();
   const int t = threadIdx.x;
-  if (t < 32 * M) {
-    const int m = t / 32, j = t % 32;
+  if (t < CW * M) {
+    const int m = t / CW, j = t % CW;
     float v = 0.f;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) v += part[q][m][j];
+    for (int q = 0; q < NW; ++q) v += part[q][m][j];
     const int n = n0 + j;
     if (n < g.n) GemvStore<T>(g, batch, m, n, v);
   }
@@ -313,7 +319,7 @@ bool GemvApplies(const GemmProblem& p) {
 
 bool GemvNNApplies(const GemmProblem& p) {
   if (p.a.dtype != QK_BF16 && p.a.dtype != QK_F16) return false;
-  if (p.m < 1 || p.m > 8 || p.a.transpose || p.b.transpose) return false;
+  if (p.m < 1 || p.m > 4 || p.a.transpose || p.b.transpose) return false;
   if (p.k % 512 != 0 || p.k == 0 || p.n % 8 != 0 || p.n == 0) return false;
   const bool batched = p.batch > 1;
   // x: 8-byte runs of four values; W: 16-byte runs of eight.
@@ -326,7 +332,7 @@ bool GemvNNApplies(const GemmProblem& p) {
       bsb % 8 != 0)
     return false;
   // W of one batch entry addressed by a 32-bit buffer offset.
-  return ((p.k - 1) * p.b.ld + p.n + 32) * 2 < (int64_t{1} << 31) &&
+  return ((p.k - 1) * p.b.ld + p.n + 64) * 2 < (int64_t{1} << 31) &&
          p.n <= (int64_t{1} << 30);
 }
 
@@ -357,18 +363,14 @@ qk_status LaunchGemv(const GemmProblem& p, hipStream_t stream) {
   g.out_f32 = p.d.dtype == QK_F32;
   const int batch = static_cast<int>(p.batch);
   if (!p.b.transpose) {
-    const dim3 gr(static_cast<unsigned>((g.n + 31) / 32), batch);
+    const dim3 gr(static_cast<unsigned>((g.n + 63) / 64), batch);
     auto go = [&](auto tag) {
       using T = decltype(tag);
       switch (g.m) {
-        case 1: gemv_nn_kernel<T, 1><<<gr, 512, 0, stream>>>(g); break;
-        case 2: gemv_nn_kernel<T, 2><<<gr, 512, 0, stream>>>(g); break;
-        case 3: gemv_nn_kernel<T, 3><<<gr, 512, 0, stream>>>(g); break;
-        case 4: gemv_nn_kernel<T, 4><<<gr, 512, 0, stream>>>(g); break;
-        case 5: gemv_nn_kernel<T, 5><<<gr, 512, 0, stream>>>(g); break;
-        case 6: gemv_nn_kernel<T, 6><<<gr, 512, 0, stream>>>(g); break;
-        case 7: gemv_nn_kernel<T, 7><<<gr, 512, 0, stream>>>(g); break;
-        default: gemv_nn_kernel<T, 8><<<gr, 512, 0, stream>>>(g); break;
+        case 1: gemv_nn_kernel<T, 1><<<gr, 1024, 0, stream>>>(g); break;
+        case 2: gemv_nn_kernel<T, 2><<<gr, 1024, 0, stream>>>(g); break;
+        case 3: gemv_nn_kernel<T, 3><<<gr, 1024, 0, stream>>>(g); break;
+        default: gemv_nn_kernel<T, 4><<<gr, 1024, 0, stream>>>(g); break;
       }
     };
     if (p.a.dtype == QK_BF16)

@@ -104,7 +104,7 @@ qk_status LaunchGemm(const GemmProblem& p, hipStream_t stream);
 // The few-row (M <= 8) f16/bf16 NT kernel (gemv.hip): whether it takes the
 // problem, and its launch.
 bool GemvApplies(const GemmProblem& p);
-// At most 8 rows of x against W stored [K][N] (gemv_nn_kernel).
+// At most 4 rows of x against W stored [K][N] (gemv_nn_kernel).
 bool GemvNNApplies(const GemmProblem& p);
 qk_status LaunchGemv(const GemmProblem& p, hipStream_t stream);
 

@@ -424,15 +424,14 @@ def test_wide_gemv_few_rows(dev, m, k):
         assert want in plan.describe(), plan.describe()
 
 
-@pytest.mark.parametrize("m", [1, 2, 5, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
 @pytest.mark.parametrize("k", [512, 2048, 8192])
 def test_gemv_nn_few_rows(dev, m, k, monkeypatch):
-    """At most eight rows of x against W stored [K][N] (N a multiple of
-    8, K of 512): the NN gemv (one workgroup per 32 columns over all of
-    K; taken by default from K = 8192, forced below it), ragged last
-    column block, both types, against the oracle."""
-    if k < 8192:
-        monkeypatch.setenv("QK_GEMV_NN", "2")
+    """At most four rows of x against W stored [K][N] (N a multiple of
+    8, K of 512): the NN gemv (one workgroup per 64 columns over all of
+    K; forced here, taken by default for weights of 2^25 values or more),
+    ragged last column block, both types, against the oracle."""
+    monkeypatch.setenv("QK_GEMV_NN", "2")
     for n, tin in ((8, "bfloat16"), (1000, "float16"), (6144, "bfloat16")):
         plan = run_case(dev, m, n, k, tin=tin, seed=m * k + n + 1)
         assert "gemv_nn" in plan.describe(), plan.describe()
@@ -447,7 +446,7 @@ def test_gemv_nn_epilogues_batches_and_layouts(dev, monkeypatch):
         plan = run_case(dev, 4, 296, 1024, epilogue=epi, separate_c=True,
                         beta=0.5, alpha=1.5)
         assert "gemv_nn" in plan.describe()
-    plan = run_case(dev, 7, 136, 512, tout="float32", pad=8, batch=3,
+    plan = run_case(dev, 3, 136, 512, tout="float32", pad=8, batch=3,
                     beta=1.0)
     assert "gemv_nn" in plan.describe()
     plan = run_case(dev, 3, 1000, 4096, batch=4, broadcast_b=True,
@@ -457,11 +456,13 @@ def test_gemv_nn_epilogues_batches_and_layouts(dev, monkeypatch):
     # split-K kernel
     assert "gemv_nn" not in run_case(dev, 4, 700, 1024).describe()
     assert "gemv_nn" not in run_case(dev, 4, 704, 1000).describe()
+    assert "gemv_nn" not in run_case(dev, 5, 704, 1024).describe()
     monkeypatch.setenv("QK_GEMV_NN", "0")
-    assert "gemv_nn" not in run_case(dev, 4, 704, 8192).describe()
+    assert "gemv_nn" not in run_case(dev, 2, 4096, 8192).describe()
     monkeypatch.delenv("QK_GEMV_NN")
-    assert "gemv_nn" in run_case(dev, 4, 704, 8192).describe()
-    assert "gemv_nn" not in run_case(dev, 4, 704, 4096).describe()
+    # by default from 2^25 weight values
+    assert "gemv_nn" in run_case(dev, 2, 4096, 8192).describe()
+    assert "gemv_nn" not in run_case(dev, 2, 4096, 4096).describe()
 
 
 def test_wide_gemv_epilogues_batches_and_layouts(dev):
